@@ -1,0 +1,168 @@
+#!/usr/bin/env python3
+"""End-to-end SCUNet-color throughput on one MI355X, with per-kernel roofline figures and
+the reference CPU path (the oracle restatement of src/cpu.rs) timed beside it.
+
+A step is one whole-image forward of SCUNet colour (in_nc 3, dim 64, config [4]*7,
+window 8, head_dim 32, seeded random-init fp32 weights) on BASELINE config 3: a
+1x3x1080x1920 seeded noisy image already resident in HBM, replicate-padded to
+1088x1920 and cropped back on the device (scunet_hip_run_device: the backend::run
+contract with pad and crop fused into the first and last convolution).
+
+value = 1920*1080 input pixels / mean step time, in Mpx/s (the reference counts input
+pixels, examples/bench.rs:191). Per-kernel device times come from HIP event pairs that
+the library records around every launch on its own stream during the timed steps.
+
+Usage: python bench.py [--gpus 1] [--steps 10] [--warmup 3] [--no-cpu-baseline]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(REPO, "scunet-rs_amd"))
+
+METRIC = "megapixels/sec end-to-end SCUNet-color 1920x1088; attention kernel TFLOP/s"
+PEAK_FP32_TFLOPS = 157.3      # MI355X dense fp32 matrix
+PEAK_HBM_GBS = 8000.0         # MI355X HBM3E
+RIDGE = PEAK_FP32_TFLOPS * 1e12 / (PEAK_HBM_GBS * 1e9)
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def roofline_of(name, launches, ms, flop, byts):
+    ai = flop / max(byts, 1.0)
+    if ai >= RIDGE:
+        ach = flop / (ms * 1e-3) / 1e12
+        return {"kernel": name, "bound": "mfma", "achieved": round(ach, 3), "peak": PEAK_FP32_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(ach / PEAK_FP32_TFLOPS, 4), "traffic": None,
+                "launches": launches, "avg_launch_ms": round(ms / launches, 5),
+                "algorithmic_flop_per_launch": flop / launches, "algorithmic_bytes_per_launch": byts / launches}
+    ach = byts / (ms * 1e-3) / 1e9
+    return {"kernel": name, "bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+            "frac": round(ach / PEAK_HBM_GBS, 4), "traffic": None, "launches": launches,
+            "avg_launch_ms": round(ms / launches, 5), "algorithmic_flop_per_launch": flop / launches,
+            "algorithmic_bytes_per_launch": byts / launches}
+
+
+def cpu_baseline(weights_path, sample_hw):
+    """The oracle (C++ restatement of the reference's src/cpu.rs) on a bounded sample."""
+    sys.path.insert(0, os.path.join(REPO, "oracle"))
+    import oracle
+    from scunet_hip import synth
+    wt = oracle.Weights.load(weights_path)
+    h, w = sample_hw
+    x = synth.noisy_image(102, 3, h, w, 50, "gradient")
+    t0 = time.perf_counter()
+    oracle.run(wt, x)
+    dt = time.perf_counter() - t0
+    return {"value": round(h * w / dt / 1e6, 5), "unit": "Mpx/s", "cores": oracle.threads(), "kind": "port",
+            "sample": f"one whole-image forward of a 1x3x{h}x{w} noisy image (BASELINE config 2 generator) "
+                      f"through oracle/scunet_oracle.cpp, the C++ restatement of src/cpu.rs; {dt:.2f} s",
+            "seconds": round(dt, 3)}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-sample", type=int, nargs=2, default=(512, 512))
+    ap.add_argument("--no-kernel-events", action="store_true",
+                    help="time the steps without the per-launch event pairs")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        log("bench.py: this build runs one image on one GPU; multi-GPU runs are not part of it "
+            "(see DESIGN.md for how a forward would shard). Use --gpus 1.")
+        sys.exit(2)
+
+    import numpy as np
+    import scunet_hip
+    from scunet_hip import synth
+
+    wpath = synth.weights_file(seed=0)
+    x = synth.config_input(3)                     # [3][1080][1920]
+    c, h, w = x.shape
+    plan = scunet_hip.Plan(h, w)
+    be = scunet_hip.Hip(wpath)
+    xp = be.malloc(x.nbytes)
+    yp = be.malloc(x.nbytes)
+    be.h2d(xp, x)
+    log(f"bench: SCUNet-color {c}x{h}x{w} (padded {plan.hp}x{plan.wp}) on {be.name()}, "
+        f"warmup {args.warmup}, steps {args.steps}")
+
+    for _ in range(args.warmup):
+        be.run_device(xp, c, h, w, yp)
+    be.synchronize()
+    be.profile(not args.no_kernel_events)
+    be.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        be.run_device(xp, c, h, w, yp)
+    be.synchronize()
+    dt = (time.perf_counter() - t0) / args.steps
+    rows = be.profile_rows() if not args.no_kernel_events else []
+    be.profile(False)
+    y = be.d2h(np.empty_like(x), yp)
+    if not np.isfinite(y).all():
+        raise RuntimeError("non-finite output")
+    mpx = h * w / dt / 1e6
+    log(f"bench: {dt * 1e3:.2f} ms/step, {mpx:.2f} Mpx/s")
+
+    kernels = []
+    for name, n, ms, flop, byts in rows:
+        kernels.append(roofline_of(name, n, ms, flop, byts))
+        kernels[-1]["share"] = round(ms / max(sum(r[2] for r in rows), 1e-9), 4)
+    for k in kernels:
+        log(f"  {k['kernel']:>14}: {k['launches']:5d} launches, {k['avg_launch_ms'] * 1e3:9.1f} us avg, "
+            f"{k['achieved']:9.2f} {k['unit']} ({100 * k['frac']:.1f}% of {k['bound']}), share {100 * k['share']:.1f}%")
+    dominant = kernels[0] if kernels else None
+    attn = next((k for k in kernels if k["kernel"] == "attention"), None)
+    attn_tflops = None
+    if attn:
+        r = next(r for r in rows if r[0] == "attention")
+        attn_tflops = round(r[3] / (r[2] * 1e-3) / 1e12, 3)
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        log(f"bench: CPU baseline (oracle) on {tuple(args.cpu_sample)} ...")
+        cpu = cpu_baseline(wpath, tuple(args.cpu_sample))
+        log(f"bench: CPU baseline {cpu['value']} Mpx/s on {cpu['cores']} threads ({cpu['seconds']} s)")
+
+    fp = be.footprint()
+    line = {
+        "metric": METRIC,
+        "value": round(mpx, 3),
+        "unit": "Mpx/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(dt * 1e3, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded noisy 1080x1920 texture, sigma 15/255; seeded random-init weights)",
+        "config": {"workload": "SCUNet-color whole-image forward, 1x3x1080x1920 replicate-padded to 1088x1920 "
+                               "(BASELINE config 3), device-resident input, pad+crop on device",
+                   "in_nc": 3, "dim": 64, "blocks": [4] * 7, "window": 8, "head_dim": 32,
+                   "kernel_events": not args.no_kernel_events},
+        "roofline": dominant,
+        "attention_tflops": attn_tflops,
+        "attention_roofline": attn,
+        "kernels": kernels,
+        "cpu_baseline": cpu,
+        "device_bytes": {"weights": fp[0], "scratch": fp[1]},
+    }
+    be.free(xp)
+    be.free(yp)
+    be.close()
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,145 @@
+/*
+ * scunet_hip.h - the C ABI of the MI355X SCUNet backend (libscunet_hip.so).
+ *
+ * This is the drop-in boundary for the reference crate's `--device gpu` path
+ * (jacobsparts/scunet-rs). Every entry point below states which reference
+ * interface it replaces. Plain pointers and sizes only; no HIP or torch types
+ * appear in any signature, so a Rust `extern "C"` block, ctypes, or any other FFI
+ * binds it directly.
+ *
+ * Conventions
+ *   - Status: 0 = OK. Non-zero = the reference's `Err(String)`; the message is
+ *     available from scunet_hip_last_error(handle) (or scunet_hip_create_error()
+ *     when there is no handle yet). Nothing here aborts on a device error or OOM.
+ *   - Planes are NCHW float32 `[c][h][w]`, the layout of Backend::forward.
+ *   - One handle per thread (the reference's `Cuda` is `&mut self`, not Sync). A
+ *     handle owns one HIP stream, created at default priority; every launch and
+ *     copy of that handle is ordered on it.
+ *   - "_device" entry points take device pointers, are stream-ordered on the
+ *     handle's stream and do not synchronize; everything else takes host pointers
+ *     and returns after the result is on the host.
+ */
+#ifndef SCUNET_HIP_H
+#define SCUNET_HIP_H
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct scunet_hip scunet_hip;
+
+/* Stage hook: called with one of the 16 stage names of cpu.rs:1175-1321
+ * ("m_head", "m_down1_blocks", "m_down1", ..., "m_tail_in", "m_tail") and that
+ * stage's plane as NCHW host floats (n elements), valid only during the call. */
+typedef void (*scunet_stage_hook)(const char* name, const float* plane, size_t n, void* user);
+
+/* --- construction (src/cuda.rs:192-241 Cuda::new, src/weights.rs:101-185 Weights::load) --- */
+
+/* Load a SCUNet safetensors checkpoint, validate its __metadata__ keys and every
+ * tensor shape exactly as weights.rs:204-280 does, and upload (repacked) to the
+ * device. Fails with a message naming the field or tensor. */
+int scunet_hip_create(const char* safetensors_path, scunet_hip** out);
+/* Message of the last failed scunet_hip_create on this thread. */
+const char* scunet_hip_create_error(void);
+void scunet_hip_destroy(scunet_hip* h);
+/* Message of the last failed call on this handle ("" if none). */
+const char* scunet_hip_last_error(const scunet_hip* h);
+
+/* Backend::name (src/backend.rs:20-21): "hip". */
+const char* scunet_hip_name(const scunet_hip* h);
+/* The architecture read from the checkpoint (weights.rs:84-98). config has 7 entries. */
+int scunet_hip_arch(const scunet_hip* h, int* in_nc, int* dim, int* head_dim, int* window,
+                    int* config);
+
+/* --- the forward (src/backend.rs:23-25 Backend::forward; src/cuda.rs:1606-1848) --- */
+
+/* x: the already replicate-padded plane [c][hp][wp] (hp, wp multiples of 64, c = in_nc);
+ * y: caller-allocated [c][hp][wp]. */
+int scunet_hip_forward(scunet_hip* h, const float* x, size_t c, size_t hp, size_t wp, float* y);
+/* Same contract on device pointers, stream-ordered, no synchronization. */
+int scunet_hip_forward_device(scunet_hip* h, const float* x, size_t c, size_t hp, size_t wp,
+                              float* y);
+/* forward with the stage hook of cpu.rs:1175-1321 (forward_dump). */
+int scunet_hip_forward_dump(scunet_hip* h, const float* x, size_t c, size_t hp, size_t wp,
+                            float* y, scunet_stage_hook hook, void* user);
+
+/* --- pad, forward, crop (src/backend.rs:63-105 backend::run; plan.rs:67-94) ---
+ * x: the image [c][hh][ww] in [0,1], any size; y: [c][hh][ww]. The replicate pad to
+ * ceil64 and the crop happen on the device, fused into the first and last convolution.
+ * Fails like plan.rs:105-118 check_min_size. */
+int scunet_hip_run(scunet_hip* h, const float* x, size_t c, size_t hh, size_t ww, float* y);
+int scunet_hip_run_device(scunet_hip* h, const float* x, size_t c, size_t hh, size_t ww, float* y);
+
+/* --- Backend's bookkeeping (src/backend.rs:30-55) --- */
+int scunet_hip_footprint(const scunet_hip* h, size_t* weight_bytes, size_t* scratch_bytes);
+int scunet_hip_release_scratch(scunet_hip* h);
+int scunet_hip_synchronize(scunet_hip* h);
+/* The handle's hipStream_t, as void*. */
+void* scunet_hip_stream(scunet_hip* h);
+
+/* Per-launch device timing (the SCUNET_PROFILE instrument of cuda.rs:106-135, 263-273,
+ * 1875-1884): when on, every launch is bracketed by a pair of HIP events on the
+ * handle's stream. profile_report synchronizes and fills up to `cap` rows of
+ * (kernel-class name, launches, total ms, algorithmic FLOP, algorithmic bytes), sorted
+ * by total time; returns the number of classes in *n. Names stay valid until the next
+ * profile call on the handle. */
+int scunet_hip_profile(scunet_hip* h, int on);
+int scunet_hip_profile_report(scunet_hip* h, const char** names, long* launches, double* ms,
+                              double* flop, double* bytes, int cap, int* n);
+
+/* --- device memory for callers without a device allocator (tests, bench) --- */
+int scunet_hip_malloc(scunet_hip* h, void** p, size_t bytes);
+int scunet_hip_free(scunet_hip* h, void* p);
+int scunet_hip_h2d(scunet_hip* h, void* dst, const void* src, size_t bytes);
+int scunet_hip_d2h(scunet_hip* h, void* dst, const void* src, size_t bytes);
+
+/* --- probes (src/cuda.rs:1153-1597), host buffers in the reference's layouts --- */
+
+/* Cuda::block_dump (cuda.rs:1153-1167): one ConvTransBlock `prefix` on x [c][hh][ww]. */
+int scunet_hip_block_probe(scunet_hip* h, const char* prefix, size_t hh, size_t ww, size_t shift,
+                           const float* x, float* out);
+/* Cuda::op_probe (cuda.rs:1173-1202): op in {"conv3x3", "conv1x1", "conv2x2s2",
+ * "conv_t2x2"} with weight `name` (+".weight", and ".bias" when present) on x
+ * [c_in][hh][ww]; out is [c_out][hh][ww] (conv2x2s2: [c_out][hh/2][ww/2], conv_t2x2:
+ * [c_out][2hh][2ww]). */
+int scunet_hip_op_probe(scunet_hip* h, const char* op, const char* name, const float* x,
+                        size_t c_in, size_t c_out, size_t hh, size_t ww, float* out);
+/* Cuda::linear_probe (cuda.rs:1471-1481): x [rows][c_in] -> out [rows][c_out]. */
+int scunet_hip_linear_probe(scunet_hip* h, const char* name, const float* x, size_t rows,
+                            size_t c_in, size_t c_out, float* out);
+/* Cuda::layer_norm_probe (cuda.rs:1484-1494): x [rows][c] -> out [rows][c]. */
+int scunet_hip_layer_norm_probe(scunet_hip* h, const char* name, const float* x, size_t rows,
+                                size_t c, float* out);
+/* Cuda::attention_kernel_probe (cuda.rs:1501-1519): the attention core alone on window-
+ * major qkv [nw*64][3c] (q | k | v column blocks, head j = columns j*hd..j*hd+hd-1 of
+ * each) with rel-pos table rp [heads][15][15]; out [nw*64][c]. The window grid is
+ * (hh/8) x (ww/8); shift > 0 applies the shifted-window mask. */
+int scunet_hip_attention_kernel_probe(scunet_hip* h, size_t hh, size_t ww, size_t c, size_t heads,
+                                      size_t hd, size_t shift, const float* qkv, const float* rp,
+                                      float* out);
+/* Cuda::gather_probe (cuda.rs:1523-1537): the window index map the attention kernel
+ * uses, x [c][hh][ww] -> tokens [nw*64][c]. */
+int scunet_hip_gather_probe(scunet_hip* h, size_t hh, size_t ww, size_t c, size_t shift,
+                            const float* x, float* tok);
+/* Cuda::window_round_trip (cuda.rs:1543-1560): gather then scatter, x -> out. */
+int scunet_hip_window_round_trip(scunet_hip* h, size_t hh, size_t ww, size_t c, size_t shift,
+                                 const float* x, float* out);
+/* Cuda::attention_probe (cuda.rs:1569-1597): gather + LN1 + qkv + attention + proj of
+ * block `prefix` on x [c][hh][ww]; returns the token buffer [nw*64][c] in window order. */
+int scunet_hip_attention_probe(scunet_hip* h, const char* prefix, size_t hh, size_t ww, size_t c,
+                               size_t shift, const float* x, float* tok);
+
+/* Cuda::bench_attn (cuda.rs:1438-1468) on device buffers: the attention core over
+ * window-major qkv [nwh*nww*64][3c] -> out [nwh*nww*64][c], rp [heads][15][15] on the
+ * host. Runs 3 warmups then `iters` launches, timed with HIP events on the handle's
+ * stream; *ms = mean device time per launch. */
+int scunet_hip_bench_attn(scunet_hip* h, const float* qkv, const float* rp, float* out, size_t nwh,
+                          size_t nww, size_t c, size_t heads, size_t shift, int iters, double* ms);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SCUNET_HIP_H */

@@ -1,0 +1,930 @@
+// The MI355X backend behind the C ABI of include/scunet_hip.h: weight upload and
+// repacking, the per-geometry device arena, the graph walker, probes, and profiling.
+//
+// The walker is the reference's Cuda::forward (src/cuda.rs:1606-1848) / cpu::forward_dump
+// (src/cpu.rs:1175-1321) stage for stage; what differs is the device's own design:
+//   * activations are pixel-major [P][c]; a block's conv half and transformer half are
+//     column ranges of one buffer, so split, concat, gather and scatter do not exist as
+//     kernels (the attention kernel reads windows through the shifted index map);
+//   * whole-plane launches, no token chunking, skips and the head stay on the device;
+//   * 9 launches per ConvTransBlock: conv1_1, 3x3+ReLU, 3x3+residual, LN1+qkv, attention,
+//     proj+residual, LN2+mlp.0+GELU, mlp.2+residual, conv1_2+residual.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "../../include/scunet_hip.h"
+#include "kernels.h"
+#include "weights.h"
+
+using namespace scunet;
+
+namespace {
+
+thread_local std::string g_create_error;
+
+const char* STAGE[7] = {"down1", "down2", "down3", "body", "up3", "up2", "up1"};
+
+struct ProfRec {
+    std::string name;
+    hipEvent_t e0, e1;
+    double flop, bytes;
+};
+
+}  // namespace
+
+struct scunet_hip {
+    Weights wt;
+    hipStream_t stream = nullptr;
+    int device = 0;
+    std::string err;
+    float scale = 0.f;
+
+    // Device weights: one allocation, name -> pointer (repacked where the kernels want it).
+    float* wblob = nullptr;
+    size_t wbytes = 0;
+    std::map<std::string, float*> w;
+    std::map<std::string, float*> tab;   // block prefix -> lane-ordered rel-pos bias table
+
+    // Arena: role -> (pointer, bytes), grown on demand, kept across calls.
+    std::map<std::string, std::pair<float*, size_t>> arena;
+
+    bool prof = false;
+    std::vector<ProfRec> recs;
+    std::vector<hipEvent_t> ev_pool;
+    size_t ev_used = 0;
+    std::vector<std::string> report_names;
+
+    ~scunet_hip() {
+        if (stream) hipStreamSynchronize(stream);
+        for (auto& kv : arena)
+            if (kv.second.first) hipFree(kv.second.first);
+        if (wblob) hipFree(wblob);
+        for (auto e : ev_pool) hipEventDestroy(e);
+        if (stream) hipStreamDestroy(stream);
+    }
+};
+
+namespace {
+
+bool fail(scunet_hip* h, const std::string& m) {
+    h->err = m;
+    return false;
+}
+
+bool ck(scunet_hip* h, hipError_t e, const char* what) {
+    if (e == hipSuccess) return true;
+    return fail(h, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+bool launched(scunet_hip* h, const char* what) {
+    return ck(h, hipGetLastError(), what);
+}
+
+float* buf(scunet_hip* h, const std::string& role, size_t floats) {
+    size_t bytes = std::max<size_t>(floats, 1) * sizeof(float);
+    auto& slot = h->arena[role];
+    if (slot.second >= bytes) return slot.first;
+    if (slot.first) {
+        hipStreamSynchronize(h->stream);
+        hipFree(slot.first);
+        slot = {nullptr, 0};
+    }
+    void* p = nullptr;
+    hipError_t e = hipMalloc(&p, bytes);
+    if (e != hipSuccess) {
+        hipGetLastError();
+        size_t held = 0;
+        for (auto& kv : h->arena) held += kv.second.second;
+        fail(h, "device allocation of " + std::to_string(bytes >> 20) + " MiB for `" + role +
+                    "` failed (" + hipGetErrorString(e) + "): " + std::to_string(held >> 20) +
+                    " MiB of scratch and " + std::to_string(h->wbytes >> 20) + " MiB of weights held");
+        return nullptr;
+    }
+    slot = {static_cast<float*>(p), bytes};
+    return slot.first;
+}
+
+// Profiling (cuda.rs:263-273): an event pair per launch when on.
+struct Span {
+    scunet_hip* h;
+    const char* name;
+    double flop, bytes;
+    hipEvent_t e0 = nullptr;
+    Span(scunet_hip* hh, const char* n, double f, double b) : h(hh), name(n), flop(f), bytes(b) {
+        if (!h->prof) return;
+        e0 = next();
+        hipEventRecord(e0, h->stream);
+    }
+    hipEvent_t next() {
+        if (h->ev_used == h->ev_pool.size()) {
+            hipEvent_t e;
+            hipEventCreate(&e);
+            h->ev_pool.push_back(e);
+        }
+        return h->ev_pool[h->ev_used++];
+    }
+    ~Span() {
+        if (!h->prof) return;
+        hipEvent_t e1 = next();
+        hipEventRecord(e1, h->stream);
+        h->recs.push_back({name, e0, e1, flop, bytes});
+    }
+};
+
+const float* W(scunet_hip* h, const std::string& name) {
+    auto it = h->w.find(name);
+    return it == h->w.end() ? nullptr : it->second;
+}
+
+// Upload every tensor once (cuda.rs:466-472 uploads lazily; here all at create), in the
+// layout its kernel reads:
+//   3x3 conv_block weights [co][ci][3][3] -> [tap][co][ci]
+//   down-conv m_downN.K.weight [co][ci][2][2] -> [co][tap*ci]        (tap = ky*2 + kx)
+//   up-conv   m_upN.0.weight  [ci][co][2][2] -> [tap*co + co'][ci]
+//   everything else as stored; rel-pos tables -> lane-ordered bias tables.
+bool upload_weights(scunet_hip* h) {
+    const Weights& wt = h->wt;
+    std::vector<std::pair<std::string, std::vector<float>>> host;
+    auto is_down = [&](const std::string& n) {
+        for (int k = 0; k < 3; ++k)
+            if (n == "m_" + std::string(STAGE[k]) + "." + std::to_string(wt.config[k]) + ".weight") return true;
+        return false;
+    };
+    auto is_up = [&](const std::string& n) {
+        for (int k = 4; k < 7; ++k)
+            if (n == "m_" + std::string(STAGE[k]) + ".0.weight") return true;
+        return false;
+    };
+    for (auto& kv : wt.all()) {
+        const std::string& n = kv.first;
+        const Tensor& t = kv.second;
+        std::vector<float> v(t.data, t.data + t.numel);
+        if (n.find(".conv_block.") != std::string::npos) {
+            size_t co = t.shape[0], ci = t.shape[1];
+            for (size_t o = 0; o < co; ++o)
+                for (size_t i = 0; i < ci; ++i)
+                    for (size_t tap = 0; tap < 9; ++tap) v[(tap * co + o) * ci + i] = t.data[(o * ci + i) * 9 + tap];
+        } else if (is_down(n)) {
+            size_t co = t.shape[0], ci = t.shape[1];
+            for (size_t o = 0; o < co; ++o)
+                for (size_t i = 0; i < ci; ++i)
+                    for (size_t tap = 0; tap < 4; ++tap) v[o * 4 * ci + tap * ci + i] = t.data[(o * ci + i) * 4 + tap];
+        } else if (is_up(n)) {
+            size_t ci = t.shape[0], co = t.shape[1];
+            for (size_t i = 0; i < ci; ++i)
+                for (size_t o = 0; o < co; ++o)
+                    for (size_t tap = 0; tap < 4; ++tap) v[(tap * co + o) * ci + i] = t.data[(i * co + o) * 4 + tap];
+        } else if (n.find("relative_position_params") != std::string::npos) {
+            int heads = int(t.shape[0]);
+            std::vector<float> tab(size_t(heads) * 64 * 64);
+            build_bias_table(t.data, heads, tab.data());
+            std::string prefix = n.substr(0, n.find(".trans_block"));
+            host.push_back({"@tab:" + prefix, std::move(tab)});
+        }
+        host.push_back({n, std::move(v)});
+    }
+    size_t total = 0;
+    for (auto& e : host) total += (e.second.size() * 4 + 255) / 256 * 256;
+    void* p = nullptr;
+    if (!ck(h, hipMalloc(&p, total), "weight upload: hipMalloc")) return false;
+    h->wblob = static_cast<float*>(p);
+    h->wbytes = total;
+    char* at = static_cast<char*>(p);
+    for (auto& e : host) {
+        if (!ck(h, hipMemcpy(at, e.second.data(), e.second.size() * 4, hipMemcpyHostToDevice), "weight upload"))
+            return false;
+        if (e.first.rfind("@tab:", 0) == 0) h->tab[e.first.substr(5)] = reinterpret_cast<float*>(at);
+        else h->w[e.first] = reinterpret_cast<float*>(at);
+        at += (e.second.size() * 4 + 255) / 256 * 256;
+    }
+    return true;
+}
+
+// Algorithmic FLOP / bytes for the profiler (fp32, 2 FLOP per multiply-add; bytes =
+// inputs read once + outputs written once).
+double gemm_flop(long M, int N, int K) { return 2.0 * double(M) * N * K; }
+
+bool run_gemm(scunet_hip* h, const char* cls, const GemmArgs& g, GemmA a, GemmE e) {
+    double bytes = 4.0 * (double(g.M) * g.K * (a == A_ADD2 ? 2 : 1) + double(g.N) * g.K +
+                          double(g.M) * g.N * (e == E_RESID ? 2 : (e == E_DUAL ? 2 : 1)));
+    Span sp(h, cls, gemm_flop(g.M, g.N, g.K), bytes);
+    const char* why = nullptr;
+    if (!gemm(g, a, e, h->stream, &why)) return fail(h, std::string(cls) + ": " + why);
+    return launched(h, cls);
+}
+
+bool run_conv3(scunet_hip* h, const Conv3Args& c, bool relu) {
+    long P = long(c.H) * c.W;
+    Span sp(h, "conv3x3", 18.0 * double(P) * c.cin * c.cout,
+            4.0 * (double(P) * (c.cin + c.cout * (relu ? 1 : 2)) + 9.0 * c.cin * c.cout));
+    const char* why = nullptr;
+    if (!conv3x3(c, relu, h->stream, &why)) return fail(h, why);
+    return launched(h, "conv3x3");
+}
+
+// Scratch of one ConvTransBlock at width t on P pixels: y [P][2t], s1 [P][t],
+// qkv [P][3t], o [P][t], hid [P][4t].
+struct BlockScratch {
+    float *y, *s1, *qkv, *o, *hid;
+};
+
+bool block_scratch(scunet_hip* h, long P, int t, BlockScratch* s) {
+    float* b = buf(h, "block", size_t(P) * 11 * t);
+    if (!b) return false;
+    s->y = b;
+    s->s1 = s->y + size_t(P) * 2 * t;
+    s->qkv = s->s1 + size_t(P) * t;
+    s->o = s->qkv + size_t(P) * 3 * t;
+    s->hid = s->o + size_t(P) * t;
+    return true;
+}
+
+// One ConvTransBlock in place on x [P][c] (cpu.rs:869-970; cuda.rs:1063-1146).
+bool block(scunet_hip* h, const std::string& p, float* x, int H, int Wd, int shift) {
+    auto dims = h->wt.block_dims(p);
+    const int t = dims.second, conv = dims.first, c = conv + t;
+    if (conv != t) return fail(h, p + ": conv and trans halves of different widths are not supported");
+    const long P = long(H) * Wd;
+    BlockScratch s;
+    if (!block_scratch(h, P, t, &s)) return false;
+    const std::string tp = p + ".trans_block";
+
+    GemmArgs g;
+    // conv1_1: y = x W^T + b.
+    g = GemmArgs{};
+    g.A = x; g.lda = c; g.W = W(h, p + ".conv1_1.weight"); g.bias = W(h, p + ".conv1_1.bias");
+    g.C = s.y; g.ldc = c; g.M = P; g.N = c; g.K = c;
+    if (!run_gemm(h, "conv1x1", g, A_ROWS, E_STORE)) return false;
+    // conv half: s1 = relu(conv3x3(y[:, :t])); y[:, :t] += conv3x3(s1).
+    Conv3Args cv;
+    cv.in = s.y; cv.ldi = c; cv.w = W(h, p + ".conv_block.0.weight"); cv.out = s.s1; cv.ldo = t;
+    cv.H = H; cv.W = Wd; cv.cin = t; cv.cout = t;
+    if (!run_conv3(h, cv, true)) return false;
+    cv.in = s.s1; cv.ldi = t; cv.w = W(h, p + ".conv_block.2.weight"); cv.out = s.y; cv.ldo = c;
+    if (!run_conv3(h, cv, false)) return false;
+    // transformer half, tokens = pixels of y[:, t:2t].
+    float* yt = s.y + t;
+    g = GemmArgs{};
+    g.A = yt; g.lda = c; g.ln_g = W(h, tp + ".ln1.weight"); g.ln_b = W(h, tp + ".ln1.bias");
+    g.W = W(h, tp + ".msa.embedding_layer.weight"); g.bias = W(h, tp + ".msa.embedding_layer.bias");
+    g.C = s.qkv; g.ldc = 3 * t; g.M = P; g.N = 3 * t; g.K = t;
+    if (!run_gemm(h, "qkv_ln", g, A_LN, E_STORE)) return false;
+    {
+        AttnArgs a;
+        a.qkv = s.qkv; a.ldq = 3 * t; a.out = s.o; a.ldo = t; a.tab = h->tab[p];
+        a.C = t; a.heads = t / h->wt.head_dim; a.nwh = H / 8; a.nww = Wd / 8; a.H = H; a.W = Wd;
+        a.shift = shift; a.pixel_mode = 1; a.scale = h->scale;
+        long nw = long(a.nwh) * a.nww;
+        Span sp(h, "attention", 16384.0 * t * nw, 4.0 * 64.0 * nw * 4 * t);
+        const char* why = nullptr;
+        if (!attention(a, h->stream, &why)) return fail(h, why);
+        if (!launched(h, "attention")) return false;
+    }
+    g = GemmArgs{};
+    g.A = s.o; g.lda = t; g.W = W(h, tp + ".msa.linear.weight"); g.bias = W(h, tp + ".msa.linear.bias");
+    g.C = yt; g.ldc = c; g.R = yt; g.ldr = c; g.M = P; g.N = t; g.K = t;
+    if (!run_gemm(h, "proj", g, A_ROWS, E_RESID)) return false;
+    g = GemmArgs{};
+    g.A = yt; g.lda = c; g.ln_g = W(h, tp + ".ln2.weight"); g.ln_b = W(h, tp + ".ln2.bias");
+    g.W = W(h, tp + ".mlp.0.weight"); g.bias = W(h, tp + ".mlp.0.bias");
+    g.C = s.hid; g.ldc = 4 * t; g.M = P; g.N = 4 * t; g.K = t;
+    if (!run_gemm(h, "mlp0_ln_gelu", g, A_LN, E_GELU)) return false;
+    g = GemmArgs{};
+    g.A = s.hid; g.lda = 4 * t; g.W = W(h, tp + ".mlp.2.weight"); g.bias = W(h, tp + ".mlp.2.bias");
+    g.C = yt; g.ldc = c; g.R = yt; g.ldr = c; g.M = P; g.N = t; g.K = 4 * t;
+    if (!run_gemm(h, "mlp2", g, A_ROWS, E_RESID)) return false;
+    // conv1_2 on the concatenation, residual over the block: x += y W^T + b.
+    g = GemmArgs{};
+    g.A = s.y; g.lda = c; g.W = W(h, p + ".conv1_2.weight"); g.bias = W(h, p + ".conv1_2.bias");
+    g.C = x; g.ldc = c; g.R = x; g.ldr = c; g.M = P; g.N = c; g.K = c;
+    return run_gemm(h, "conv1x1", g, A_ROWS, E_RESID);
+}
+
+bool dump_plane(scunet_hip* h, scunet_stage_hook hook, void* user, const char* name, const float* plane,
+                int c, long P) {
+    if (!hook) return true;
+    float* tmp = buf(h, "dump", size_t(c) * P);
+    if (!tmp) return false;
+    nhwc_to_nchw(plane, tmp, c, P, c, h->stream);
+    if (!launched(h, "dump")) return false;
+    std::vector<float> host(size_t(c) * P);
+    if (!ck(h, hipMemcpyAsync(host.data(), tmp, host.size() * 4, hipMemcpyDeviceToHost, h->stream), "dump D2H"))
+        return false;
+    if (!ck(h, hipStreamSynchronize(h->stream), "dump sync")) return false;
+    hook(name, host.data(), host.size(), user);
+    return true;
+}
+
+// The walker. x: NCHW image of size hh x ww (hh == H, ww == W when already padded);
+// y: NCHW [in_nc][oh][ow] (the crop is fused into m_tail).
+bool walk(scunet_hip* h, const float* x, int hh, int ww, int H, int Wd, float* y, int oh, int ow,
+          scunet_stage_hook hook, void* user) {
+    const Weights& wt = h->wt;
+    const int dim = wt.dim, in_nc = wt.in_nc;
+    if (H % 64 || Wd % 64) return fail(h, "the padded plane must be a multiple of 64 on each axis");
+    long P[4];
+    int Hs[4], Ws[4];
+    for (int k = 0; k < 4; ++k) {
+        Hs[k] = H >> k;
+        Ws[k] = Wd >> k;
+        P[k] = long(Hs[k]) * Ws[k];
+    }
+    float* cur[4];
+    float* skip[4] = {nullptr, nullptr, nullptr, nullptr};
+    for (int k = 0; k < 4; ++k) {
+        cur[k] = buf(h, "cur" + std::to_string(k), size_t(P[k]) * (dim << k));
+        if (!cur[k]) return false;
+        if (k > 0) {
+            skip[k] = buf(h, "skip" + std::to_string(k), size_t(P[k]) * (dim << k));
+            if (!skip[k]) return false;
+        }
+    }
+    {
+        Span sp(h, "head", 2.0 * 9 * in_nc * dim * double(P[0]), 4.0 * (in_nc + dim) * double(P[0]));
+        head_conv(x, in_nc, hh, ww, H, Wd, W(h, "m_head.0.weight"), dim, cur[0], false, h->stream);
+        if (!launched(h, "m_head")) return false;
+    }
+    if (!dump_plane(h, hook, user, "m_head", cur[0], dim, P[0])) return false;
+    for (int k = 0; k < 3; ++k) {
+        const std::string name = STAGE[k];
+        const int count = wt.config[k];
+        const int c = dim << k;
+        for (int i = 0; i < count; ++i)
+            if (!block(h, "m_" + name + "." + std::to_string(i), cur[k], Hs[k], Ws[k], (i & 1) ? wt.window / 2 : 0))
+                return false;
+        if (!dump_plane(h, hook, user, ("m_" + name + "_blocks").c_str(), cur[k], c, P[k])) return false;
+        GemmArgs g;
+        g.A = cur[k]; g.lda = c; g.W = W(h, "m_" + name + "." + std::to_string(count) + ".weight");
+        g.C = skip[k + 1]; g.C2 = cur[k + 1]; g.ldc = 2 * c; g.M = P[k + 1]; g.N = 2 * c; g.K = 4 * c;
+        g.in_w = Ws[k]; g.cin = c;
+        if (!run_gemm(h, "down2x2", g, A_S2D, E_DUAL)) return false;
+        if (!dump_plane(h, hook, user, ("m_" + name).c_str(), skip[k + 1], 2 * c, P[k + 1])) return false;
+    }
+    for (int i = 0; i < wt.config[3]; ++i)
+        if (!block(h, "m_body." + std::to_string(i), cur[3], Hs[3], Ws[3], (i & 1) ? wt.window / 2 : 0))
+            return false;
+    if (!dump_plane(h, hook, user, "m_body", cur[3], dim << 3, P[3])) return false;
+    for (int k = 0; k < 3; ++k) {
+        const std::string name = STAGE[4 + k];
+        const int lvl = 2 - k;               // up3 -> level 2, up2 -> 1, up1 -> 0
+        const int co = dim << lvl, ci = 2 * co;
+        GemmArgs g;
+        g.A = cur[lvl + 1]; g.A2 = skip[lvl + 1]; g.lda = ci;
+        g.W = W(h, "m_" + name + ".0.weight");
+        g.C = cur[lvl]; g.M = P[lvl + 1]; g.N = 4 * co; g.K = ci; g.in_w = Ws[lvl + 1]; g.cout = co;
+        if (!run_gemm(h, "up2x2", g, A_ADD2, E_D2S)) return false;
+        if (!dump_plane(h, hook, user, ("m_" + name + "_up").c_str(), cur[lvl], co, P[lvl])) return false;
+        for (int i = 0; i < wt.config[4 + k]; ++i)
+            if (!block(h, "m_" + name + "." + std::to_string(i + 1), cur[lvl], Hs[lvl], Ws[lvl],
+                       (i & 1) ? wt.window / 2 : 0))
+                return false;
+        if (!dump_plane(h, hook, user, ("m_" + name).c_str(), cur[lvl], co, P[lvl])) return false;
+    }
+    {
+        Span sp(h, "head", 2.0 * 9 * in_nc * dim * double(P[0]), 4.0 * (in_nc + 2 * dim) * double(P[0]));
+        head_conv(x, in_nc, hh, ww, H, Wd, W(h, "m_head.0.weight"), dim, cur[0], true, h->stream);
+        if (!launched(h, "m_head (tail input)")) return false;
+    }
+    if (!dump_plane(h, hook, user, "m_tail_in", cur[0], dim, P[0])) return false;
+    {
+        Span sp(h, "tail", 2.0 * 9 * in_nc * dim * double(P[0]), 4.0 * (in_nc + dim) * double(P[0]));
+        if (!tail_conv(cur[0], dim, H, Wd, W(h, "m_tail.0.weight"), in_nc, y, oh, ow, h->stream))
+            return fail(h, "m_tail: unsupported width");
+        if (!launched(h, "m_tail")) return false;
+    }
+    if (hook) {
+        std::vector<float> host(size_t(in_nc) * oh * ow);
+        if (!ck(h, hipMemcpyAsync(host.data(), y, host.size() * 4, hipMemcpyDeviceToHost, h->stream), "dump D2H"))
+            return false;
+        if (!ck(h, hipStreamSynchronize(h->stream), "dump sync")) return false;
+        hook("m_tail", host.data(), host.size(), user);
+    }
+    return true;
+}
+
+bool check_arch(scunet_hip* h) {
+    const Weights& wt = h->wt;
+    if (wt.window != 8) return fail(h, "window " + std::to_string(wt.window) + ": the attention kernel is built for 8x8 windows");
+    if (wt.head_dim != 32) return fail(h, "head_dim " + std::to_string(wt.head_dim) + ": the attention kernel is built for head_dim 32");
+    if (wt.in_nc > 4) return fail(h, "in_nc > 4 is not supported by the m_tail kernel");
+    if (wt.dim != 64) return fail(h, "dim " + std::to_string(wt.dim) + ": only the published dim = 64 is supported");
+    return true;
+}
+
+size_t pad64(size_t v) { return (v + 63) / 64 * 64; }
+
+// plan.rs:105-118.
+bool check_min_size(scunet_hip* h, size_t hh, size_t ww) {
+    size_t hp = pad64(hh), wp = pad64(ww), win = size_t(h->wt.window);
+    if (hh == 0 || ww == 0) return fail(h, "empty image");
+    if (hp < 8 * win || wp < 8 * win)
+        return fail(h, std::to_string(hh) + "x" + std::to_string(ww) + " pads to " + std::to_string(hp) + "x" +
+                           std::to_string(wp) + ", but the 1/8-resolution body needs at least " +
+                           std::to_string(win) + "x" + std::to_string(win) + " pixels there");
+    return true;
+}
+
+template <typename F>
+int guard(scunet_hip* h, F&& f) {
+    if (!h) return -1;
+    h->err.clear();
+    try {
+        return f() ? 0 : 1;
+    } catch (const std::exception& e) {
+        h->err = e.what();
+        return 1;
+    }
+}
+
+bool to_device(scunet_hip* h, const char* role, const float* src, size_t n, float** out) {
+    *out = buf(h, role, n);
+    if (!*out) return false;
+    return ck(h, hipMemcpyAsync(*out, src, n * 4, hipMemcpyHostToDevice, h->stream), "H2D");
+}
+
+bool to_host(scunet_hip* h, float* dst, const float* src, size_t n) {
+    if (!ck(h, hipMemcpyAsync(dst, src, n * 4, hipMemcpyDeviceToHost, h->stream), "D2H")) return false;
+    return ck(h, hipStreamSynchronize(h->stream), "sync");
+}
+
+bool shape_ok(scunet_hip* h, size_t c, size_t hp, size_t wp) {
+    if (c != size_t(h->wt.in_nc))
+        return fail(h, "expected " + std::to_string(h->wt.in_nc) + " channels, got " + std::to_string(c));
+    if (hp % 64 || wp % 64 || hp == 0 || wp == 0)
+        return fail(h, "forward takes the padded plane: " + std::to_string(hp) + "x" + std::to_string(wp) +
+                           " is not a multiple of 64 on each axis");
+    return true;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* scunet_hip_create_error(void) { return g_create_error.c_str(); }
+
+int scunet_hip_create(const char* path, scunet_hip** out) {
+    g_create_error.clear();
+    if (!out) {
+        g_create_error = "null output handle";
+        return 1;
+    }
+    *out = nullptr;
+    std::unique_ptr<scunet_hip> h(new scunet_hip());
+    std::string err;
+    if (!h->wt.load(path ? path : "", &err)) {
+        g_create_error = err;
+        return 1;
+    }
+    if (!check_arch(h.get())) {
+        g_create_error = h->err;
+        return 1;
+    }
+    int ndev = 0;
+    hipError_t e = hipGetDeviceCount(&ndev);
+    if (e != hipSuccess || ndev == 0) {
+        g_create_error = std::string("no HIP device: ") + hipGetErrorString(e);
+        return 1;
+    }
+    hipGetDevice(&h->device);
+    if (hipStreamCreateWithFlags(&h->stream, hipStreamNonBlocking) != hipSuccess) {
+        g_create_error = "hipStreamCreate failed";
+        return 1;
+    }
+    h->scale = std::pow(float(h->wt.head_dim), -0.5f);
+    if (!upload_weights(h.get())) {
+        g_create_error = h->err;
+        return 1;
+    }
+    *out = h.release();
+    return 0;
+}
+
+void scunet_hip_destroy(scunet_hip* h) { delete h; }
+
+const char* scunet_hip_last_error(const scunet_hip* h) { return h ? h->err.c_str() : "null handle"; }
+
+const char* scunet_hip_name(const scunet_hip*) { return "hip"; }
+
+int scunet_hip_arch(const scunet_hip* h, int* in_nc, int* dim, int* head_dim, int* window, int* config) {
+    if (!h) return -1;
+    if (in_nc) *in_nc = h->wt.in_nc;
+    if (dim) *dim = h->wt.dim;
+    if (head_dim) *head_dim = h->wt.head_dim;
+    if (window) *window = h->wt.window;
+    if (config)
+        for (int i = 0; i < 7; ++i) config[i] = h->wt.config[i];
+    return 0;
+}
+
+int scunet_hip_forward_device(scunet_hip* h, const float* x, size_t c, size_t hp, size_t wp, float* y) {
+    return guard(h, [&] {
+        if (!shape_ok(h, c, hp, wp)) return false;
+        return walk(h, x, int(hp), int(wp), int(hp), int(wp), y, int(hp), int(wp), nullptr, nullptr);
+    });
+}
+
+int scunet_hip_forward_dump(scunet_hip* h, const float* x, size_t c, size_t hp, size_t wp, float* y,
+                            scunet_stage_hook hook, void* user) {
+    return guard(h, [&] {
+        if (!shape_ok(h, c, hp, wp)) return false;
+        size_t n = c * hp * wp;
+        float *dx, *dy;
+        if (!to_device(h, "io_x", x, n, &dx)) return false;
+        dy = buf(h, "io_y", n);
+        if (!dy) return false;
+        if (!walk(h, dx, int(hp), int(wp), int(hp), int(wp), dy, int(hp), int(wp), hook, user)) return false;
+        return to_host(h, y, dy, n);
+    });
+}
+
+int scunet_hip_forward(scunet_hip* h, const float* x, size_t c, size_t hp, size_t wp, float* y) {
+    return scunet_hip_forward_dump(h, x, c, hp, wp, y, nullptr, nullptr);
+}
+
+int scunet_hip_run_device(scunet_hip* h, const float* x, size_t c, size_t hh, size_t ww, float* y) {
+    return guard(h, [&] {
+        if (!check_min_size(h, hh, ww)) return false;
+        if (c != size_t(h->wt.in_nc))
+            return fail(h, "expected " + std::to_string(h->wt.in_nc) + " channels, got " + std::to_string(c));
+        size_t hp = pad64(hh), wp = pad64(ww);
+        return walk(h, x, int(hh), int(ww), int(hp), int(wp), y, int(hh), int(ww), nullptr, nullptr);
+    });
+}
+
+int scunet_hip_run(scunet_hip* h, const float* x, size_t c, size_t hh, size_t ww, float* y) {
+    return guard(h, [&] {
+        if (!check_min_size(h, hh, ww)) return false;
+        if (c != size_t(h->wt.in_nc))
+            return fail(h, "expected " + std::to_string(h->wt.in_nc) + " channels, got " + std::to_string(c));
+        size_t hp = pad64(hh), wp = pad64(ww), n = c * hh * ww;
+        float *dx, *dy;
+        if (!to_device(h, "io_x", x, n, &dx)) return false;
+        dy = buf(h, "io_y", n);
+        if (!dy) return false;
+        if (!walk(h, dx, int(hh), int(ww), int(hp), int(wp), dy, int(hh), int(ww), nullptr, nullptr)) return false;
+        return to_host(h, y, dy, n);
+    });
+}
+
+int scunet_hip_footprint(const scunet_hip* h, size_t* weight_bytes, size_t* scratch_bytes) {
+    if (!h) return -1;
+    size_t s = 0;
+    for (auto& kv : h->arena) s += kv.second.second;
+    if (weight_bytes) *weight_bytes = h->wbytes;
+    if (scratch_bytes) *scratch_bytes = s;
+    return 0;
+}
+
+int scunet_hip_release_scratch(scunet_hip* h) {
+    return guard(h, [&] {
+        if (!ck(h, hipStreamSynchronize(h->stream), "sync")) return false;
+        for (auto& kv : h->arena)
+            if (kv.second.first) hipFree(kv.second.first);
+        h->arena.clear();
+        return true;
+    });
+}
+
+int scunet_hip_synchronize(scunet_hip* h) {
+    return guard(h, [&] { return ck(h, hipStreamSynchronize(h->stream), "hipStreamSynchronize"); });
+}
+
+void* scunet_hip_stream(scunet_hip* h) { return h ? static_cast<void*>(h->stream) : nullptr; }
+
+int scunet_hip_profile(scunet_hip* h, int on) {
+    return guard(h, [&] {
+        if (!ck(h, hipStreamSynchronize(h->stream), "sync")) return false;
+        h->prof = on != 0;
+        h->recs.clear();
+        h->ev_used = 0;
+        return true;
+    });
+}
+
+int scunet_hip_profile_report(scunet_hip* h, const char** names, long* launches, double* ms, double* flop,
+                              double* bytes, int cap, int* n) {
+    return guard(h, [&] {
+        if (!ck(h, hipStreamSynchronize(h->stream), "sync")) return false;
+        struct Agg { long n = 0; double ms = 0, flop = 0, bytes = 0; };
+        std::map<std::string, Agg> agg;
+        for (auto& r : h->recs) {
+            float t = 0.f;
+            if (!ck(h, hipEventElapsedTime(&t, r.e0, r.e1), "hipEventElapsedTime")) return false;
+            auto& a = agg[r.name];
+            a.n += 1;
+            a.ms += t;
+            a.flop += r.flop;
+            a.bytes += r.bytes;
+        }
+        std::vector<std::pair<std::string, Agg>> v(agg.begin(), agg.end());
+        std::sort(v.begin(), v.end(), [](auto& a, auto& b) { return a.second.ms > b.second.ms; });
+        h->report_names.clear();
+        for (auto& e : v) h->report_names.push_back(e.first);
+        int k = 0;
+        for (; k < int(v.size()) && k < cap; ++k) {
+            if (names) names[k] = h->report_names[size_t(k)].c_str();
+            if (launches) launches[k] = v[size_t(k)].second.n;
+            if (ms) ms[k] = v[size_t(k)].second.ms;
+            if (flop) flop[k] = v[size_t(k)].second.flop;
+            if (bytes) bytes[k] = v[size_t(k)].second.bytes;
+        }
+        if (n) *n = int(v.size());
+        h->recs.clear();
+        h->ev_used = 0;
+        return true;
+    });
+}
+
+int scunet_hip_malloc(scunet_hip* h, void** p, size_t bytes) {
+    return guard(h, [&] { return ck(h, hipMalloc(p, std::max<size_t>(bytes, 1)), "hipMalloc"); });
+}
+int scunet_hip_free(scunet_hip* h, void* p) {
+    return guard(h, [&] {
+        if (!ck(h, hipStreamSynchronize(h->stream), "sync")) return false;
+        return ck(h, hipFree(p), "hipFree");
+    });
+}
+int scunet_hip_h2d(scunet_hip* h, void* dst, const void* src, size_t bytes) {
+    return guard(h, [&] {
+        if (!ck(h, hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, h->stream), "H2D")) return false;
+        return ck(h, hipStreamSynchronize(h->stream), "sync");
+    });
+}
+int scunet_hip_d2h(scunet_hip* h, void* dst, const void* src, size_t bytes) {
+    return guard(h, [&] {
+        if (!ck(h, hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, h->stream), "D2H")) return false;
+        return ck(h, hipStreamSynchronize(h->stream), "sync");
+    });
+}
+
+// ---------------------------------------------------------------------------
+// Probes
+// ---------------------------------------------------------------------------
+
+int scunet_hip_block_probe(scunet_hip* h, const char* prefix, size_t hh, size_t ww, size_t shift, const float* x,
+                           float* out) {
+    return guard(h, [&] {
+        std::string p = prefix;
+        if (!h->wt.has(p + ".conv1_1.weight")) return fail(h, "no block `" + p + "`");
+        if (hh % 8 || ww % 8 || hh == 0 || ww == 0) return fail(h, "block planes must be multiples of 8");
+        auto d = h->wt.block_dims(p);
+        int c = d.first + d.second;
+        long P = long(hh) * long(ww);
+        float *dx, *xt;
+        if (!to_device(h, "probe_in", x, size_t(c) * P, &dx)) return false;
+        xt = buf(h, "probe_x", size_t(c) * P);
+        if (!xt) return false;
+        nchw_to_nhwc(dx, xt, c, P, c, h->stream);
+        if (!block(h, p, xt, int(hh), int(ww), int(shift))) return false;
+        float* o = buf(h, "probe_out", size_t(c) * P);
+        if (!o) return false;
+        nhwc_to_nchw(xt, o, c, P, c, h->stream);
+        if (!launched(h, "block probe")) return false;
+        return to_host(h, out, o, size_t(c) * P);
+    });
+}
+
+int scunet_hip_op_probe(scunet_hip* h, const char* op, const char* name, const float* x, size_t c_in, size_t c_out,
+                        size_t hh, size_t ww, float* out) {
+    return guard(h, [&] {
+        std::string o = op, n = name;
+        const float* wp = W(h, n + ".weight");
+        if (!wp) return fail(h, "no weight `" + n + ".weight`");
+        const float* bp = W(h, n + ".bias");
+        long P = long(hh) * long(ww);
+        float* dx;
+        if (!to_device(h, "probe_in", x, c_in * size_t(P), &dx)) return false;
+        float* xt = buf(h, "probe_x", c_in * size_t(P));
+        if (!xt) return false;
+        long Po = P;
+        if (o == "conv2x2s2") Po = P / 4;
+        if (o == "conv_t2x2") Po = P * 4;
+        float* yt = buf(h, "probe_y", c_out * size_t(Po));
+        float* yo = buf(h, "probe_out", c_out * size_t(Po));
+        if (!yt || !yo) return false;
+        if (o == "conv3x3" && n == "m_head.0") {
+            head_conv(dx, int(c_in), int(hh), int(ww), int(hh), int(ww), wp, int(c_out), yt, false, h->stream);
+        } else if (o == "conv3x3" && n == "m_tail.0") {
+            nchw_to_nhwc(dx, xt, int(c_in), P, long(c_in), h->stream);
+            if (!tail_conv(xt, int(c_in), int(hh), int(ww), wp, int(c_out), yo, int(hh), int(ww), h->stream))
+                return fail(h, "m_tail: unsupported width");
+            if (!launched(h, "op probe")) return false;
+            return to_host(h, out, yo, c_out * size_t(P));
+        } else {
+            nchw_to_nhwc(dx, xt, int(c_in), P, long(c_in), h->stream);
+            if (o == "conv3x3") {
+                Conv3Args cv;
+                cv.in = xt; cv.ldi = long(c_in); cv.w = wp; cv.out = yt; cv.ldo = long(c_out);
+                cv.H = int(hh); cv.W = int(ww); cv.cin = int(c_in); cv.cout = int(c_out);
+                if (!ck(h, hipMemsetAsync(yt, 0, c_out * size_t(P) * 4, h->stream), "memset")) return false;
+                if (!run_conv3(h, cv, false)) return false;
+            } else {
+                GemmArgs g;
+                g.A = xt; g.lda = long(c_in); g.W = wp; g.C = yt; g.ldc = long(c_out);
+                g.N = int(c_out);
+                if (o == "conv1x1") {
+                    g.bias = bp; g.M = P; g.K = int(c_in);
+                    if (!run_gemm(h, "conv1x1", g, A_ROWS, E_STORE)) return false;
+                } else if (o == "conv2x2s2") {
+                    g.M = P / 4; g.K = int(4 * c_in); g.in_w = int(ww); g.cin = int(c_in);
+                    if (!run_gemm(h, "down2x2", g, A_S2D, E_STORE)) return false;
+                } else if (o == "conv_t2x2") {
+                    g.M = P; g.K = int(c_in); g.N = int(4 * c_out); g.in_w = int(ww); g.cout = int(c_out);
+                    g.ldc = 0;
+                    float* zero = buf(h, "probe_zero", c_in * size_t(P));
+                    if (!zero) return false;
+                    if (!ck(h, hipMemsetAsync(zero, 0, c_in * size_t(P) * 4, h->stream), "memset")) return false;
+                    g.A2 = zero;
+                    if (!run_gemm(h, "up2x2", g, A_ADD2, E_D2S)) return false;
+                } else {
+                    return fail(h, "op_probe: no such op `" + o + "`");
+                }
+            }
+        }
+        nhwc_to_nchw(yt, yo, int(c_out), Po, long(c_out), h->stream);
+        if (!launched(h, "op probe")) return false;
+        return to_host(h, out, yo, c_out * size_t(Po));
+    });
+}
+
+int scunet_hip_linear_probe(scunet_hip* h, const char* name, const float* x, size_t rows, size_t c_in, size_t c_out,
+                            float* out) {
+    return guard(h, [&] {
+        std::string n = name;
+        const float* wp = W(h, n + ".weight");
+        if (!wp) return fail(h, "no weight `" + n + ".weight`");
+        float* dx;
+        if (!to_device(h, "probe_in", x, rows * c_in, &dx)) return false;
+        float* y = buf(h, "probe_out", rows * c_out);
+        if (!y) return false;
+        GemmArgs g;
+        g.A = dx; g.lda = long(c_in); g.W = wp; g.bias = W(h, n + ".bias"); g.C = y; g.ldc = long(c_out);
+        g.M = long(rows); g.N = int(c_out); g.K = int(c_in);
+        if (!run_gemm(h, "linear", g, A_ROWS, E_STORE)) return false;
+        return to_host(h, out, y, rows * c_out);
+    });
+}
+
+// LayerNorm through the GEMM's own LN prologue against an identity weight: every output
+// is one normalised value times 1 plus zeros, so the GEMM adds nothing of its own.
+int scunet_hip_layer_norm_probe(scunet_hip* h, const char* name, const float* x, size_t rows, size_t c, float* out) {
+    return guard(h, [&] {
+        std::string n = name;
+        const float* gw = W(h, n + ".weight");
+        const float* gb = W(h, n + ".bias");
+        if (!gw || !gb) return fail(h, "no LayerNorm `" + n + "`");
+        float* dx;
+        if (!to_device(h, "probe_in", x, rows * c, &dx)) return false;
+        std::vector<float> eye(c * c, 0.f);
+        for (size_t i = 0; i < c; ++i) eye[i * c + i] = 1.f;
+        float* de;
+        if (!to_device(h, "probe_eye", eye.data(), c * c, &de)) return false;
+        float* y = buf(h, "probe_out", rows * c);
+        if (!y) return false;
+        GemmArgs g;
+        g.A = dx; g.lda = long(c); g.ln_g = gw; g.ln_b = gb; g.W = de; g.C = y; g.ldc = long(c);
+        g.M = long(rows); g.N = int(c); g.K = int(c);
+        if (!run_gemm(h, "layer_norm", g, A_LN, E_STORE)) return false;
+        return to_host(h, out, y, rows * c);
+    });
+}
+
+int scunet_hip_attention_kernel_probe(scunet_hip* h, size_t hh, size_t ww, size_t c, size_t heads, size_t hd,
+                                      size_t shift, const float* qkv, const float* rp, float* out) {
+    return guard(h, [&] {
+        if (hd != 32 || c != heads * hd) return fail(h, "the attention kernel needs head_dim 32");
+        if (hh % 8 || ww % 8) return fail(h, "the plane must be a multiple of the 8x8 window");
+        size_t nw = (hh / 8) * (ww / 8), nt = nw * 64;
+        float *dq, *dt;
+        if (!to_device(h, "probe_in", qkv, nt * 3 * c, &dq)) return false;
+        std::vector<float> tab(heads * 64 * 64);
+        build_bias_table(rp, int(heads), tab.data());
+        if (!to_device(h, "probe_tab", tab.data(), tab.size(), &dt)) return false;
+        float* y = buf(h, "probe_out", nt * c);
+        if (!y) return false;
+        AttnArgs a;
+        a.qkv = dq; a.ldq = long(3 * c); a.out = y; a.ldo = long(c); a.tab = dt; a.C = int(c); a.heads = int(heads);
+        a.nwh = int(hh / 8); a.nww = int(ww / 8); a.H = int(hh); a.W = int(ww); a.shift = int(shift);
+        a.pixel_mode = 0; a.scale = std::pow(float(hd), -0.5f);
+        const char* why = nullptr;
+        if (!attention(a, h->stream, &why)) return fail(h, why);
+        if (!launched(h, "attention probe")) return false;
+        return to_host(h, out, y, nt * c);
+    });
+}
+
+int scunet_hip_gather_probe(scunet_hip* h, size_t hh, size_t ww, size_t c, size_t shift, const float* x, float* tok) {
+    return guard(h, [&] {
+        if (hh % 8 || ww % 8) return fail(h, "the plane must be a multiple of the 8x8 window");
+        long P = long(hh) * long(ww);
+        float* dx;
+        if (!to_device(h, "probe_in", x, c * size_t(P), &dx)) return false;
+        float* xt = buf(h, "probe_x", c * size_t(P));
+        float* y = buf(h, "probe_out", c * size_t(P));
+        if (!xt || !y) return false;
+        nchw_to_nhwc(dx, xt, int(c), P, long(c), h->stream);
+        window_gather(xt, y, int(c), int(hh), int(ww), int(shift), h->stream);
+        if (!launched(h, "gather probe")) return false;
+        return to_host(h, tok, y, c * size_t(P));
+    });
+}
+
+int scunet_hip_window_round_trip(scunet_hip* h, size_t hh, size_t ww, size_t c, size_t shift, const float* x,
+                                 float* out) {
+    return guard(h, [&] {
+        if (hh % 8 || ww % 8) return fail(h, "the plane must be a multiple of the 8x8 window");
+        long P = long(hh) * long(ww);
+        float* dx;
+        if (!to_device(h, "probe_in", x, c * size_t(P), &dx)) return false;
+        float* xt = buf(h, "probe_x", c * size_t(P));
+        float* tk = buf(h, "probe_y", c * size_t(P));
+        float* y = buf(h, "probe_out", c * size_t(P));
+        if (!xt || !tk || !y) return false;
+        nchw_to_nhwc(dx, xt, int(c), P, long(c), h->stream);
+        window_gather(xt, tk, int(c), int(hh), int(ww), int(shift), h->stream);
+        hipMemsetAsync(xt, 0, c * size_t(P) * 4, h->stream);
+        window_scatter(tk, xt, int(c), int(hh), int(ww), int(shift), h->stream);
+        nhwc_to_nchw(xt, y, int(c), P, long(c), h->stream);
+        if (!launched(h, "round trip")) return false;
+        return to_host(h, out, y, c * size_t(P));
+    });
+}
+
+int scunet_hip_attention_probe(scunet_hip* h, const char* prefix, size_t hh, size_t ww, size_t c, size_t shift,
+                               const float* x, float* tok) {
+    return guard(h, [&] {
+        std::string tp = std::string(prefix) + ".trans_block";
+        if (!W(h, tp + ".ln1.weight")) return fail(h, "no block `" + std::string(prefix) + "`");
+        if (hh % 8 || ww % 8) return fail(h, "the plane must be a multiple of the 8x8 window");
+        long P = long(hh) * long(ww);
+        int t = int(c);
+        float* dx;
+        if (!to_device(h, "probe_in", x, c * size_t(P), &dx)) return false;
+        float* xt = buf(h, "probe_x", c * size_t(P));
+        float* qkv = buf(h, "probe_qkv", 3 * c * size_t(P));
+        float* att = buf(h, "probe_att", c * size_t(P));
+        float* o = buf(h, "probe_y", c * size_t(P));
+        float* y = buf(h, "probe_out", c * size_t(P));
+        if (!xt || !qkv || !att || !o || !y) return false;
+        nchw_to_nhwc(dx, xt, t, P, t, h->stream);
+        GemmArgs g;
+        g.A = xt; g.lda = t; g.ln_g = W(h, tp + ".ln1.weight"); g.ln_b = W(h, tp + ".ln1.bias");
+        g.W = W(h, tp + ".msa.embedding_layer.weight"); g.bias = W(h, tp + ".msa.embedding_layer.bias");
+        g.C = qkv; g.ldc = 3 * t; g.M = P; g.N = 3 * t; g.K = t;
+        if (!run_gemm(h, "qkv_ln", g, A_LN, E_STORE)) return false;
+        AttnArgs a;
+        a.qkv = qkv; a.ldq = 3 * t; a.out = att; a.ldo = t; a.tab = h->tab[prefix]; a.C = t;
+        a.heads = t / h->wt.head_dim; a.nwh = int(hh / 8); a.nww = int(ww / 8); a.H = int(hh); a.W = int(ww);
+        a.shift = int(shift); a.pixel_mode = 1; a.scale = h->scale;
+        const char* why = nullptr;
+        if (!attention(a, h->stream, &why)) return fail(h, why);
+        g = GemmArgs{};
+        g.A = att; g.lda = t; g.W = W(h, tp + ".msa.linear.weight"); g.bias = W(h, tp + ".msa.linear.bias");
+        g.C = o; g.ldc = t; g.M = P; g.N = t; g.K = t;
+        if (!run_gemm(h, "proj", g, A_ROWS, E_STORE)) return false;
+        window_gather(o, y, t, int(hh), int(ww), int(shift), h->stream);
+        if (!launched(h, "attention probe")) return false;
+        return to_host(h, tok, y, c * size_t(P));
+    });
+}
+
+int scunet_hip_bench_attn(scunet_hip* h, const float* qkv, const float* rp, float* out, size_t nwh, size_t nww,
+                          size_t c, size_t heads, size_t shift, int iters, double* ms) {
+    return guard(h, [&] {
+        if (c != heads * 32) return fail(h, "the attention kernel needs head_dim 32");
+        std::vector<float> tab(heads * 64 * 64);
+        build_bias_table(rp, int(heads), tab.data());
+        float* dt;
+        if (!to_device(h, "bench_tab", tab.data(), tab.size(), &dt)) return false;
+        AttnArgs a;
+        a.qkv = qkv; a.ldq = long(3 * c); a.out = out; a.ldo = long(c); a.tab = dt; a.C = int(c);
+        a.heads = int(heads); a.nwh = int(nwh); a.nww = int(nww); a.H = int(nwh * 8); a.W = int(nww * 8);
+        a.shift = int(shift); a.pixel_mode = 0; a.scale = h->scale;
+        const char* why = nullptr;
+        for (int i = 0; i < 3; ++i)
+            if (!attention(a, h->stream, &why)) return fail(h, why);
+        hipEvent_t e0, e1;
+        hipEventCreate(&e0);
+        hipEventCreate(&e1);
+        hipEventRecord(e0, h->stream);
+        for (int i = 0; i < iters; ++i) attention(a, h->stream, &why);
+        hipEventRecord(e1, h->stream);
+        bool ok = launched(h, "attention bench") && ck(h, hipEventSynchronize(e1), "sync");
+        float t = 0.f;
+        if (ok) ok = ck(h, hipEventElapsedTime(&t, e0, e1), "elapsed");
+        hipEventDestroy(e0);
+        hipEventDestroy(e1);
+        if (ok && ms) *ms = double(t) / std::max(iters, 1);
+        return ok;
+    });
+}
+
+}  // extern "C"

@@ -1,0 +1,101 @@
+// Launchers for the gfx950 kernels (kernels.hip). Host code only sees these.
+//
+// Activation layout on the device is pixel-major ("NHWC"): element (pixel p, channel c)
+// of a plane with row stride ld lives at base[p * ld + c], p = y * W + x. A block's
+// conv half and transformer half are the column ranges [0, t) and [t, 2t) of one
+// [P][2t] buffer, so the split and the concatenation of the reference
+// (cpu.rs:867-868) cost nothing.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+
+namespace scunet {
+
+// A-operand loaders of the GEMM.
+enum GemmA {
+    A_ROWS = 0,   // A[m][k] = A[m*lda + k]
+    A_LN = 1,     // LayerNorm(A row)[k] (eps 1e-5, gamma/beta), K = the row width (<= 256)
+    A_S2D = 2,    // 2x2 stride-2 patches: A[m][tap*cin + ci] = in[(2y+ky, 2x+kx)][ci]
+    A_ADD2 = 3,   // A[m][k] = A[m*lda + k] + A2[m*lda + k] (the skip join before an up-conv)
+};
+// Epilogues (bias is always added; out = sum_k A[m][k] W[n][k] + bias[n]).
+enum GemmE {
+    E_STORE = 0,  // C[m*ldc + n] = out
+    E_DUAL = 1,   // C and C2 both (the down-conv output that is also the stage skip)
+    E_GELU = 2,   // C = gelu_erf(out)
+    E_RESID = 3,  // C[m*ldc + n] = R[m*ldr + n] + out (C may equal R: in place)
+    E_D2S = 4,    // 2x2 transposed conv: n = tap*cout + co -> out pixel (2i+dy, 2j+dx)
+};
+
+struct GemmArgs {
+    const float* A = nullptr;
+    const float* A2 = nullptr;
+    long lda = 0;
+    const float* W = nullptr;      // [N][K] row-major
+    const float* bias = nullptr;   // [N] or null
+    const float* ln_g = nullptr;
+    const float* ln_b = nullptr;
+    float* C = nullptr;
+    float* C2 = nullptr;
+    long ldc = 0;
+    const float* R = nullptr;
+    long ldr = 0;
+    long M = 0;
+    int N = 0, K = 0;
+    int in_w = 0;   // A_S2D: input plane width; E_D2S: input plane width
+    int cin = 0;    // A_S2D
+    int cout = 0;   // E_D2S
+};
+
+// Returns false (and a reason) if no tile configuration fits the shape.
+bool gemm(const GemmArgs& g, GemmA a, GemmE e, hipStream_t s, const char** why);
+
+struct Conv3Args {
+    const float* in = nullptr;
+    long ldi = 0;                  // channels [0, cin) of a [P][ldi] plane
+    const float* w = nullptr;      // repacked [9][cout][cin]
+    float* out = nullptr;
+    long ldo = 0;
+    int H = 0, W = 0, cin = 0, cout = 0;
+};
+// relu=true: out = relu(conv); relu=false: out += conv (the conv half's residual).
+bool conv3x3(const Conv3Args& a, bool relu, hipStream_t s, const char** why);
+
+struct AttnArgs {
+    const float* qkv = nullptr;    // rows of [q | k | v], each C wide
+    long ldq = 0;
+    float* out = nullptr;          // rows of C
+    long ldo = 0;
+    const float* tab = nullptr;    // [heads][64 lanes][64] rel-pos bias in lane order
+    int C = 0, heads = 0;
+    int nwh = 0, nww = 0;          // window grid
+    int H = 0, W = 0;              // plane (pixel mode)
+    int shift = 0;
+    int pixel_mode = 1;            // 1: rows are pixels y*W+x; 0: rows are window*64+token
+    float scale = 0.f;
+};
+// 8x8 windows, head_dim 32 only.
+bool attention(const AttnArgs& a, hipStream_t s, const char** why);
+// Host-side construction of the lane-ordered bias table from rp [heads][15][15].
+void build_bias_table(const float* rp, int heads, float* tab);
+
+// m_head (in_nc -> dim, 3x3, zero pad) reading an NCHW image of size hh x ww that is
+// replicate-padded on the fly to H x W; writes (or, with add, accumulates into) the
+// pixel-major [H*W][dim] plane.
+bool head_conv(const float* x, int cin, int hh, int ww, int H, int W, const float* w, int dim,
+               float* out, bool add, hipStream_t s);
+// m_tail (dim -> cout, 3x3, zero pad) from pixel-major [H*W][dim] into NCHW [cout][oh][ow]
+// for the top-left oh x ow corner (oh <= H, ow <= W: the crop is fused).
+bool tail_conv(const float* in, int dim, int H, int W, const float* w, int cout, float* out,
+               int oh, int ow, hipStream_t s);
+
+// Layout changes for the host boundary, probes and stage dumps.
+void nchw_to_nhwc(const float* src, float* dst, int c, long P, long ld, hipStream_t s);
+void nhwc_to_nchw(const float* src, float* dst, int c, long P, long ld, hipStream_t s);
+// The window index map: tok[(wi*64 + t)*c + ch] = x[pix(wi, t)*c + ch] and its inverse.
+void window_gather(const float* x, float* tok, int c, int H, int W, int shift, hipStream_t s);
+void window_scatter(const float* tok, float* x, int c, int H, int W, int shift, hipStream_t s);
+
+}  // namespace scunet

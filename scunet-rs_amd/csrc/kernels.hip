@@ -1,0 +1,737 @@
+// gfx950 (MI355X, CDNA4) kernels of the SCUNet forward. All arithmetic is fp32; every
+// contraction runs on the fp32 matrix cores through v_mfma_f32_16x16x4_f32.
+//
+// MFMA 16x16x4 f32 operand/result layout (wave64, lane l, li = l % 16, lg = l / 16):
+//   A operand: lane holds A[li][lg]       (16 x 4)
+//   B operand: lane holds B[lg][li]       (4 x 16)
+//   C/D      : lane holds C[4*lg + r][li] for r = 0..3 (4 accumulator registers)
+// The K order inside a 16-wide slice is permuted so that each lane fetches 4
+// consecutive k values with one 16-byte load: at MFMA step s the lane with group lg
+// supplies k = 16*kk + 4*lg + s for both operands. Any K permutation is valid as long
+// as A and B agree on it.
+#include "kernels.h"
+
+#include <cmath>
+#include <cstdint>
+
+namespace scunet {
+
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+#define DEVI __device__ __forceinline__
+
+DEVI f4 mfma4(float a, float b, f4 c) { return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0); }
+
+DEVI f4 ld4(const float* p) { return *reinterpret_cast<const f4*>(p); }
+DEVI void st4(float* p, f4 v) { *reinterpret_cast<f4*>(p) = v; }
+
+// Workgroups are dispatched round-robin over the 8 XCDs (workgroup b runs on XCD b % 8),
+// and each XCD has its own L2. Remap so every XCD processes one contiguous range of
+// logical tiles: tiles that share an input (the N-blocks of one M-tile, neighbouring
+// spatial tiles) then meet in the same L2.
+DEVI long xcd_swizzle(long b, long nb) {
+    long q = nb >> 3, r = nb & 7;
+    long xcd = b & 7, j = b >> 3;
+    long start = xcd < r ? xcd * (q + 1) : r * (q + 1) + (xcd - r) * q;
+    return start + j;
+}
+
+// GELU with the Abramowitz & Stegun 7.1.26 erf the reference's CPU path uses
+// (cpu.rs:293-332), evaluated in fp32 (|erf error| < 1.5e-7 + fp32 rounding).
+DEVI float gelu_as(float v) {
+    float x = v * 0.70710678118654752440f;
+    float t = 1.0f / (1.0f + 0.3275911f * fabsf(x));
+    float y = 1.0f - (((((1.061405429f * t - 1.453152027f) * t) + 1.421413741f) * t - 0.284496736f) * t +
+                      0.254829592f) * t * __expf(-x * x);
+    float e = x >= 0.0f ? y : -y;
+    return 0.5f * v * (1.0f + e);
+}
+
+// ---------------------------------------------------------------------------
+// GEMM: C[m][n] = epi(sum_k A[m][k] W[n][k] + bias[n]), M pixels, N and K small.
+// Tile BM x BN x 32, 256 threads = 4 waves, each wave WM x WN of 16x16 MFMA tiles.
+// Global -> registers (prefetch of the next K slice) -> LDS -> MFMA.
+// ---------------------------------------------------------------------------
+template <int BM, int BN, int WM, int WN, int AM, int EP>
+__global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
+    constexpr int BK = 32, LDK = BK + 4;   // +4 floats: ds_read_b128 rows hit distinct banks
+    constexpr int NWN = BN / WN;
+    constexpr int MT = WM / 16, NT = WN / 16;
+    constexpr int AV = BM * BK / 4 / 256;  // float4 per thread per A slice
+    constexpr int BV = (BN * BK / 4 + 255) / 256;
+    static_assert((BM / WM) * (BN / WN) == 4, "4 waves");
+    static_assert(AV >= 1, "BM too small");
+    __shared__ float As[BM * LDK];
+    __shared__ float Bs[BN * LDK];
+    __shared__ float s_mu[AM == A_LN ? BM : 1];
+    __shared__ float s_rs[AM == A_LN ? BM : 1];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int li = lane & 15, lg = lane >> 4;
+    const int ntn = g.N / BN;
+    const long tile = xcd_swizzle(blockIdx.x, gridDim.x);
+    const long m0 = (tile / ntn) * BM;
+    const int n0 = int(tile % ntn) * BN;
+    const int wm = wave / NWN, wn = wave % NWN;
+
+    if constexpr (AM == A_LN) {
+        // Row statistics, two-pass as cpu.rs:338-357: mu = sum/K, var = sum (x-mu)^2 / K.
+        const int L = g.K >> 2;            // lanes per row (K <= 256 -> L <= 64)
+        const int rpp = 64 / L;            // rows per pass
+        const int per_wave = BM / 4;
+        for (int base = 0; base < per_wave; base += rpp) {
+            int r = wave * per_wave + base + lane / L;
+            int j = lane % L;
+            long gm = m0 + r;
+            f4 v = {0.f, 0.f, 0.f, 0.f};
+            bool ok = (base + lane / L) < per_wave && gm < g.M;
+            if (ok) v = ld4(g.A + gm * g.lda + j * 4);
+            float s = (v.x + v.y) + (v.z + v.w);
+            for (int o = L >> 1; o > 0; o >>= 1) s += __shfl_xor(s, o);
+            float mu = s / float(g.K);
+            f4 d = v - mu;
+            float q = (d.x * d.x + d.y * d.y) + (d.z * d.z + d.w * d.w);
+            for (int o = L >> 1; o > 0; o >>= 1) q += __shfl_xor(q, o);
+            float var = q / float(g.K);
+            if (j == 0 && (base + lane / L) < per_wave) {
+                s_mu[r] = mu;
+                s_rs[r] = 1.0f / sqrtf(var + 1e-5f);
+            }
+        }
+        __syncthreads();
+    }
+
+    f4 ra[AV], rb[BV];
+    auto load = [&](int k0) {
+#pragma unroll
+        for (int i = 0; i < AV; ++i) {
+            int f = tid + i * 256;
+            int row = f >> 3, c4 = f & 7;
+            long gm = m0 + row;
+            int k = k0 + c4 * 4;
+            f4 v = {0.f, 0.f, 0.f, 0.f};
+            if (gm < g.M) {
+                if constexpr (AM == A_S2D) {
+                    int tap = k / g.cin, ci = k - tap * g.cin;
+                    int ow = g.in_w >> 1;
+                    long oy = gm / ow, ox = gm - oy * ow;
+                    long ip = (2 * oy + (tap >> 1)) * long(g.in_w) + 2 * ox + (tap & 1);
+                    v = ld4(g.A + ip * g.cin + ci);
+                } else if constexpr (AM == A_ADD2) {
+                    v = ld4(g.A + gm * g.lda + k) + ld4(g.A2 + gm * g.lda + k);
+                } else {
+                    v = ld4(g.A + gm * g.lda + k);
+                }
+            }
+            ra[i] = v;
+        }
+#pragma unroll
+        for (int i = 0; i < BV; ++i) {
+            int f = tid + i * 256;
+            if (f < BN * 8) {
+                int row = f >> 3, c4 = f & 7;
+                rb[i] = ld4(g.W + long(n0 + row) * g.K + k0 + c4 * 4);
+            }
+        }
+    };
+    auto stash = [&](int k0) {
+#pragma unroll
+        for (int i = 0; i < AV; ++i) {
+            int f = tid + i * 256;
+            int row = f >> 3, c4 = f & 7;
+            f4 v = ra[i];
+            if constexpr (AM == A_LN) {
+                int k = k0 + c4 * 4;
+                float mu = s_mu[row], rs = s_rs[row];
+                f4 gg = ld4(g.ln_g + k), bb = ld4(g.ln_b + k);
+                v = (v - mu) * rs * gg + bb;
+                if (m0 + row >= g.M) v = f4{0.f, 0.f, 0.f, 0.f};
+            }
+            st4(&As[row * LDK + c4 * 4], v);
+        }
+#pragma unroll
+        for (int i = 0; i < BV; ++i) {
+            int f = tid + i * 256;
+            if (f < BN * 8) {
+                int row = f >> 3, c4 = f & 7;
+                st4(&Bs[row * LDK + c4 * 4], rb[i]);
+            }
+        }
+    };
+
+    f4 acc[MT][NT];
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int j = 0; j < NT; ++j) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
+
+    load(0);
+    stash(0);
+    __syncthreads();
+    for (int k0 = 0; k0 < g.K; k0 += BK) {
+        const bool more = k0 + BK < g.K;
+        if (more) load(k0 + BK);
+#pragma unroll
+        for (int kk = 0; kk < BK / 16; ++kk) {
+            f4 a[MT], b[NT];
+#pragma unroll
+            for (int i = 0; i < MT; ++i) a[i] = ld4(&As[(wm * WM + i * 16 + li) * LDK + kk * 16 + lg * 4]);
+#pragma unroll
+            for (int j = 0; j < NT; ++j) b[j] = ld4(&Bs[(wn * WN + j * 16 + li) * LDK + kk * 16 + lg * 4]);
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
+#pragma unroll
+                for (int i = 0; i < MT; ++i)
+#pragma unroll
+                    for (int j = 0; j < NT; ++j) acc[i][j] = mfma4(a[i][s], b[j][s], acc[i][j]);
+        }
+        __syncthreads();
+        if (more) {
+            stash(k0 + BK);
+            __syncthreads();
+        }
+    }
+
+    // Epilogue: lane holds rows 4*lg + r of each 16x16 tile, column li.
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+        const int col = n0 + wn * WN + j * 16 + li;
+        const float bv = g.bias ? g.bias[col] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < MT; ++i) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const long row = m0 + wm * WM + i * 16 + lg * 4 + r;
+                if (row >= g.M) continue;
+                float v = acc[i][j][r] + bv;
+                if constexpr (EP == E_STORE) {
+                    g.C[row * g.ldc + col] = v;
+                } else if constexpr (EP == E_DUAL) {
+                    g.C[row * g.ldc + col] = v;
+                    g.C2[row * g.ldc + col] = v;
+                } else if constexpr (EP == E_GELU) {
+                    g.C[row * g.ldc + col] = gelu_as(v);
+                } else if constexpr (EP == E_RESID) {
+                    g.C[row * g.ldc + col] = g.R[row * g.ldr + col] + v;
+                } else {  // E_D2S
+                    long ii = row / g.in_w, jj = row - ii * g.in_w;
+                    int tap = col / g.cout, co = col - tap * g.cout;
+                    long oy = 2 * ii + (tap >> 1), ox = 2 * jj + (tap & 1);
+                    g.C[(oy * 2 * g.in_w + ox) * g.cout + co] = v;
+                }
+            }
+        }
+    }
+}
+
+template <int BM, int BN, int WM, int WN, int AM>
+static void launch_gemm_e(const GemmArgs& g, GemmE e, hipStream_t s) {
+    long tiles = ((g.M + BM - 1) / BM) * (g.N / BN);
+    dim3 grid{unsigned(tiles), 1u, 1u}, block{256u, 1u, 1u};
+    switch (e) {
+        case E_STORE: hipLaunchKernelGGL((k_gemm<BM, BN, WM, WN, AM, E_STORE>), grid, block, 0, s, g); break;
+        case E_DUAL: hipLaunchKernelGGL((k_gemm<BM, BN, WM, WN, AM, E_DUAL>), grid, block, 0, s, g); break;
+        case E_GELU: hipLaunchKernelGGL((k_gemm<BM, BN, WM, WN, AM, E_GELU>), grid, block, 0, s, g); break;
+        case E_RESID: hipLaunchKernelGGL((k_gemm<BM, BN, WM, WN, AM, E_RESID>), grid, block, 0, s, g); break;
+        case E_D2S: hipLaunchKernelGGL((k_gemm<BM, BN, WM, WN, AM, E_D2S>), grid, block, 0, s, g); break;
+    }
+}
+
+template <int BM, int BN, int WM, int WN>
+static void launch_gemm_a(const GemmArgs& g, GemmA a, GemmE e, hipStream_t s) {
+    switch (a) {
+        case A_ROWS: launch_gemm_e<BM, BN, WM, WN, A_ROWS>(g, e, s); break;
+        case A_LN: launch_gemm_e<BM, BN, WM, WN, A_LN>(g, e, s); break;
+        case A_S2D: launch_gemm_e<BM, BN, WM, WN, A_S2D>(g, e, s); break;
+        case A_ADD2: launch_gemm_e<BM, BN, WM, WN, A_ADD2>(g, e, s); break;
+    }
+}
+
+bool gemm(const GemmArgs& g, GemmA a, GemmE e, hipStream_t s, const char** why) {
+    if (g.M <= 0) return true;
+    if (g.K % 32 != 0) { *why = "gemm: K must be a multiple of 32"; return false; }
+    if (a == A_LN && (g.K > 256 || (g.K & (g.K - 1)) != 0)) {
+        *why = "gemm: the LayerNorm prologue needs K a power of two <= 256";
+        return false;
+    }
+    if (a == A_S2D && (g.cin % 32 != 0 || g.K != 4 * g.cin || (g.in_w & 1))) {
+        *why = "gemm: space-to-depth needs cin % 32 == 0, K == 4 cin, even width";
+        return false;
+    }
+    if (e == E_D2S && (g.cout % 16 != 0 || g.N != 4 * g.cout)) {
+        *why = "gemm: depth-to-space needs cout % 16 == 0 and N == 4 cout";
+        return false;
+    }
+    if (g.N % 128 == 0) launch_gemm_a<128, 128, 64, 64>(g, a, e, s);
+    else if (g.N % 96 == 0) launch_gemm_a<128, 96, 32, 96>(g, a, e, s);
+    else if (g.N % 64 == 0) launch_gemm_a<256, 64, 64, 64>(g, a, e, s);
+    else if (g.N % 32 == 0) launch_gemm_a<256, 32, 64, 32>(g, a, e, s);
+    else { *why = "gemm: N must be a multiple of 32"; return false; }
+    return true;
+}
+
+// ---------------------------------------------------------------------------
+// 3x3 convolution, stride 1, zero padding 1, no bias, as an implicit GEMM:
+// M = a 16x16 tile of output pixels, N = BN output channels, K = 9 taps x cin.
+// Each 16-channel input slice of the tile's 18x18 halo and the matching weights go
+// through LDS; a wave owns 4 tile rows (4 M-tiles of 16 pixels) x BN channels.
+// ---------------------------------------------------------------------------
+template <int BN, bool RELU>
+__global__ __launch_bounds__(256) void k_conv3x3(Conv3Args a) {
+    constexpr int BK = 16, LDC = BK + 4, HW = 18;
+    constexpr int NT = BN / 16;
+    constexpr int HV = (HW * HW * 4 + 255) / 256;   // halo float4 per thread
+    constexpr int WV = (9 * BN * 4 + 255) / 256;    // weight float4 per thread
+    __shared__ float Hs[HW * HW * LDC];
+    __shared__ float Ws[9 * BN * LDC];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int li = lane & 15, lg = lane >> 4;
+    const int tx = (a.W + 15) >> 4, ty = (a.H + 15) >> 4, nb = a.cout / BN;
+    const long tile = xcd_swizzle(blockIdx.x, gridDim.x);
+    const int nblk = int(tile % nb);
+    const long sp = tile / nb;
+    const int y0 = int(sp / tx) * 16, x0 = int(sp % tx) * 16;
+    const int co0 = nblk * BN;
+    (void)ty;
+
+    f4 rh[HV], rw[WV];
+    auto load = [&](int ci0) {
+#pragma unroll
+        for (int i = 0; i < HV; ++i) {
+            int f = tid + i * 256;
+            f4 v = {0.f, 0.f, 0.f, 0.f};
+            if (f < HW * HW * 4) {
+                int px = f >> 2, c4 = f & 3;
+                int gy = y0 - 1 + px / HW, gx = x0 - 1 + px % HW;
+                if (gy >= 0 && gy < a.H && gx >= 0 && gx < a.W)
+                    v = ld4(a.in + (long(gy) * a.W + gx) * a.ldi + ci0 + c4 * 4);
+            }
+            rh[i] = v;
+        }
+#pragma unroll
+        for (int i = 0; i < WV; ++i) {
+            int f = tid + i * 256;
+            if (f < 9 * BN * 4) {
+                int tap = f / (BN * 4), rem = f - tap * (BN * 4);
+                int n = rem >> 2, c4 = rem & 3;
+                rw[i] = ld4(a.w + (long(tap) * a.cout + co0 + n) * a.cin + ci0 + c4 * 4);
+            }
+        }
+    };
+    auto stash = [&]() {
+#pragma unroll
+        for (int i = 0; i < HV; ++i) {
+            int f = tid + i * 256;
+            if (f < HW * HW * 4) st4(&Hs[(f >> 2) * LDC + (f & 3) * 4], rh[i]);
+        }
+#pragma unroll
+        for (int i = 0; i < WV; ++i) {
+            int f = tid + i * 256;
+            if (f < 9 * BN * 4) {
+                int tap = f / (BN * 4), rem = f - tap * (BN * 4);
+                st4(&Ws[(tap * BN + (rem >> 2)) * LDC + (rem & 3) * 4], rw[i]);
+            }
+        }
+    };
+
+    f4 acc[4][NT];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < NT; ++j) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
+
+    load(0);
+    stash();
+    __syncthreads();
+    for (int ci0 = 0; ci0 < a.cin; ci0 += BK) {
+        const bool more = ci0 + BK < a.cin;
+        if (more) load(ci0 + BK);
+#pragma unroll
+        for (int tap = 0; tap < 9; ++tap) {
+            const int ky = tap / 3, kx = tap % 3;
+            f4 av[4], bv[NT];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) av[i] = ld4(&Hs[((wave * 4 + i + ky) * HW + li + kx) * LDC + lg * 4]);
+#pragma unroll
+            for (int j = 0; j < NT; ++j) bv[j] = ld4(&Ws[(tap * BN + j * 16 + li) * LDC + lg * 4]);
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+#pragma unroll
+                    for (int j = 0; j < NT; ++j) acc[i][j] = mfma4(av[i][s], bv[j][s], acc[i][j]);
+        }
+        __syncthreads();
+        if (more) {
+            stash();
+            __syncthreads();
+        }
+    }
+
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int y = y0 + wave * 4 + i;
+        if (y >= a.H) continue;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int x = x0 + lg * 4 + r;
+            if (x >= a.W) continue;
+            float* o = a.out + (long(y) * a.W + x) * a.ldo + co0 + li;
+#pragma unroll
+            for (int j = 0; j < NT; ++j) {
+                float v = acc[i][j][r];
+                if constexpr (RELU) o[j * 16] = fmaxf(v, 0.0f);
+                else o[j * 16] += v;
+            }
+        }
+    }
+}
+
+bool conv3x3(const Conv3Args& a, bool relu, hipStream_t s, const char** why) {
+    if (a.cin % 16 != 0) { *why = "conv3x3: cin must be a multiple of 16"; return false; }
+    long tiles = long((a.W + 15) / 16) * ((a.H + 15) / 16);
+    if (a.cout % 64 == 0) {
+        dim3 grid(unsigned(tiles * (a.cout / 64)));
+        if (relu) hipLaunchKernelGGL((k_conv3x3<64, true>), grid, dim3(256), 0, s, a);
+        else hipLaunchKernelGGL((k_conv3x3<64, false>), grid, dim3(256), 0, s, a);
+    } else if (a.cout % 32 == 0) {
+        dim3 grid(unsigned(tiles * (a.cout / 32)));
+        if (relu) hipLaunchKernelGGL((k_conv3x3<32, true>), grid, dim3(256), 0, s, a);
+        else hipLaunchKernelGGL((k_conv3x3<32, false>), grid, dim3(256), 0, s, a);
+    } else {
+        *why = "conv3x3: cout must be a multiple of 32";
+        return false;
+    }
+    return true;
+}
+
+// ---------------------------------------------------------------------------
+// Window attention, 8x8 windows (64 tokens), head_dim 32. One wave per (window, head).
+//   S^T = K Q^T on MFMA (keys are the M rows, queries the N columns), so after the
+//   product each lane holds, for ONE query, 16 of its 64 key logits; the other 48
+//   are in the lanes 16, 32 and 48 away. Softmax: max and sum over the 16 values and a
+//   two-step xor shuffle. The probabilities are then exactly the A operand of
+//   O = P V (lane = query row, registers = 4 consecutive keys of the lane's key group),
+//   so no data moves between the two products and nothing goes through LDS.
+// Logit = (q.k) * scale + bias[h][p][q]; masked -> -FLT_MAX/4 (cpu.rs:365-370, 681-683).
+// ---------------------------------------------------------------------------
+DEVI long win_row(const AttnArgs& a, long wi, int t, int wh, int ww) {
+    if (!a.pixel_mode) return wi * 64 + t;
+    int y = wh * 8 + (t >> 3) + a.shift;
+    int x = ww * 8 + (t & 7) + a.shift;
+    if (y >= a.H) y -= a.H;
+    if (x >= a.W) x -= a.W;
+    return long(y) * a.W + x;
+}
+
+__global__ __launch_bounds__(256) void k_attention(AttnArgs a, long units) {
+    const int lane = threadIdx.x & 63;
+    const long u = long(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    if (u >= units) return;                      // whole wave exits together
+    const int li = lane & 15, lg = lane >> 4;
+    const long wi = u / a.heads;
+    const int h = int(u - wi * a.heads);
+    const int wh = int(wi / a.nww), ww = int(wi - long(wh) * a.nww);
+    const int hoff = h * 32;
+    const float* q_base = a.qkv + hoff;
+    const float* k_base = a.qkv + a.C + hoff;
+    const float* v_base = a.qkv + 2 * a.C + hoff;
+
+    // K fragments: key tile mt (rows 16mt + li), dim group G (dims 16G + 4lg .. +3).
+    f4 kf[4][2];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+        long row = win_row(a, wi, mt * 16 + li, wh, ww);
+#pragma unroll
+        for (int G = 0; G < 2; ++G) kf[mt][G] = ld4(k_base + row * a.ldq + G * 16 + lg * 4);
+    }
+    // V as the B operand of P V: key 16kt + 4lg + r, dim 16nd + li.
+    float vv[4][4][2];
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            long row = win_row(a, wi, kt * 16 + lg * 4 + r, wh, ww);
+#pragma unroll
+            for (int nd = 0; nd < 2; ++nd) vv[kt][r][nd] = v_base[row * a.ldq + nd * 16 + li];
+        }
+
+    const bool masked = a.shift > 0;
+    const bool row_edge = masked && wh == a.nwh - 1;
+    const bool col_edge = masked && ww == a.nww - 1;
+    const float* tab = a.tab + (long(h) * 64 + lane) * 64;
+    const float SENT = -3.4028234663852886e38f / 4.0f;
+
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) {
+        long qrow = win_row(a, wi, nt * 16 + li, wh, ww);
+        f4 qf[2];
+#pragma unroll
+        for (int G = 0; G < 2; ++G) qf[G] = ld4(q_base + qrow * a.ldq + G * 16 + lg * 4);
+        f4 S[4];
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) S[mt] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int G = 0; G < 2; ++G)
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
+#pragma unroll
+                for (int mt = 0; mt < 4; ++mt) S[mt] = mfma4(kf[mt][G][s], qf[G][s], S[mt]);
+
+        // Logits for query 16nt + li against keys 16mt + 4lg + r.
+        const bool q_row_lo = nt < 2;
+        const bool q_col_lo = (li & 7) < 4;
+        const bool k_col_lo = (lg & 1) == 0;
+        float mx = -INFINITY;
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+            f4 b = ld4(tab + nt * 16 + mt * 4);
+            const bool k_row_lo = mt < 2;
+            const bool hit = (row_edge && (q_row_lo != k_row_lo)) || (col_edge && (q_col_lo != k_col_lo));
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                float v = S[mt][r] * a.scale + b[r];
+                if (hit) v = SENT;
+                S[mt][r] = v;
+                mx = fmaxf(mx, v);
+            }
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 16));
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        float sum = 0.0f;
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                float e = __expf(S[mt][r] - mx);
+                S[mt][r] = e;
+                sum += e;
+            }
+        sum += __shfl_xor(sum, 16);
+        sum += __shfl_xor(sum, 32);
+        const float inv = 1.0f / sum;
+
+        f4 O[2] = {f4{0.f, 0.f, 0.f, 0.f}, f4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                float p = S[kt][r] * inv;
+#pragma unroll
+                for (int nd = 0; nd < 2; ++nd) O[nd] = mfma4(p, vv[kt][r][nd], O[nd]);
+            }
+        // O lane layout: query 16nt + 4lg + r, dim 16nd + li.
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            long orow = win_row(a, wi, nt * 16 + lg * 4 + r, wh, ww);
+            float* o = a.out + orow * a.ldo + hoff + li;
+            o[0] = O[0][r];
+            o[16] = O[1][r];
+        }
+    }
+}
+
+bool attention(const AttnArgs& a, hipStream_t s, const char** why) {
+    if (a.C != a.heads * 32) { *why = "attention: head_dim must be 32"; return false; }
+    long units = long(a.nwh) * a.nww * a.heads;
+    if (units == 0) return true;
+    dim3 grid(unsigned((units + 3) / 4));
+    hipLaunchKernelGGL(k_attention, grid, dim3(256), 0, s, a, units);
+    return true;
+}
+
+void build_bias_table(const float* rp, int heads, float* tab) {
+    // tab[h][lane][nt][mt][r] = B_h[query 16nt + lane%16][key 16mt + 4(lane/16) + r],
+    // B_h[p][q] = rp[h][(p/8 - q/8 + 7)][(p%8 - q%8 + 7)]   (cpu.rs:532-546).
+    for (int h = 0; h < heads; ++h)
+        for (int lane = 0; lane < 64; ++lane)
+            for (int nt = 0; nt < 4; ++nt)
+                for (int mt = 0; mt < 4; ++mt)
+                    for (int r = 0; r < 4; ++r) {
+                        int p = nt * 16 + (lane & 15);
+                        int q = mt * 16 + (lane >> 4) * 4 + r;
+                        int dy = p / 8 - q / 8 + 7, dx = p % 8 - q % 8 + 7;
+                        tab[((long(h) * 64 + lane) * 4 + nt) * 16 + mt * 4 + r] = rp[h * 225 + dy * 15 + dx];
+                    }
+}
+
+// ---------------------------------------------------------------------------
+// m_head: in_nc -> dim 3x3 from the NCHW image, replicate padding to H x W folded into
+// the reads (plan.rs:67-82) and zero padding outside the plane (cpu.rs:66-71). Terms
+// are added channel, ky, kx ascending with separate multiply and add, as cpu.rs:99-127
+// does, so this stage reproduces the reference bit for bit.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_head(const float* __restrict__ x, int cin, int hh, int ww,
+                                              int H, int W, const float* __restrict__ w, int dim,
+                                              float* __restrict__ out, int add, long total) {
+#pragma clang fp contract(off)
+    extern __shared__ float sw[];
+    for (int i = threadIdx.x; i < dim * cin * 9; i += 256) sw[i] = w[i];
+    __syncthreads();
+    const int groups = dim >> 2;
+    long gid = long(blockIdx.x) * 256 + threadIdx.x;
+    if (gid >= total) return;
+    long p = gid / groups;
+    int cg = int(gid - p * groups);
+    int y = int(p / W), xx = int(p - long(y) * W);
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int ci = 0; ci < cin; ++ci) {
+        const float* plane = x + long(ci) * hh * ww;
+        for (int ky = 0; ky < 3; ++ky) {
+            int sy = y + ky - 1;
+            if (sy < 0 || sy >= H) continue;
+            int cy = sy < hh ? sy : hh - 1;
+            for (int kx = 0; kx < 3; ++kx) {
+                int sx = xx + kx - 1;
+                if (sx < 0 || sx >= W) continue;
+                int cx = sx < ww ? sx : ww - 1;
+                float v = plane[long(cy) * ww + cx];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    float k = sw[((cg * 4 + j) * cin + ci) * 9 + ky * 3 + kx];
+                    acc[j] = acc[j] + k * v;   // contraction is off: a multiply, then an add
+                }
+            }
+        }
+    }
+    float* o = out + p * dim + cg * 4;
+    f4 r = {acc[0], acc[1], acc[2], acc[3]};
+    if (add) r = ld4(o) + r;
+    st4(o, r);
+}
+
+bool head_conv(const float* x, int cin, int hh, int ww, int H, int W, const float* w, int dim,
+               float* out, bool add, hipStream_t s) {
+    long total = long(H) * W * (dim / 4);
+    size_t shm = size_t(dim) * cin * 9 * sizeof(float);
+    hipLaunchKernelGGL(k_head, dim3(unsigned((total + 255) / 256)), dim3(256), shm, s, x, cin, hh, ww,
+                       H, W, w, dim, out, add ? 1 : 0, total);
+    return true;
+}
+
+// ---------------------------------------------------------------------------
+// m_tail: dim -> cout 3x3 from the pixel-major plane into NCHW, cropped to oh x ow.
+// A 16x16 output tile; 16-channel slices of the 18x18 halo go through LDS; one thread
+// per output pixel accumulates all cout (<= 4) outputs, channel, ky, kx ascending.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_tail(const float* __restrict__ in, int dim, int H, int W,
+                                              const float* __restrict__ w, int cout, float* __restrict__ out,
+                                              int oh, int ow) {
+    constexpr int HW = 18, CH = 16, LDC = CH + 1;
+    __shared__ float hs[HW * HW * LDC];
+    __shared__ float sw[4 * 64 * 9];
+    for (int i = threadIdx.x; i < cout * dim * 9; i += 256) sw[i] = w[i];
+    const int tx = (W + 15) / 16;
+    const int y0 = int(blockIdx.x / tx) * 16, x0 = int(blockIdx.x % tx) * 16;
+    const int ly = threadIdx.x >> 4, lx = threadIdx.x & 15;
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int c0 = 0; c0 < dim; c0 += CH) {
+        __syncthreads();
+        for (int f = threadIdx.x; f < HW * HW * CH; f += 256) {
+            int px = f / CH, c = f % CH;
+            int gy = y0 - 1 + px / HW, gx = x0 - 1 + px % HW;
+            float v = 0.f;
+            if (gy >= 0 && gy < H && gx >= 0 && gx < W) v = in[(long(gy) * W + gx) * dim + c0 + c];
+            hs[px * LDC + c] = v;
+        }
+        __syncthreads();
+        for (int c = 0; c < CH; ++c)
+            for (int ky = 0; ky < 3; ++ky)
+                for (int kx = 0; kx < 3; ++kx) {
+                    float v = hs[((ly + ky) * HW + lx + kx) * LDC + c];
+                    for (int o = 0; o < cout; ++o) acc[o] += sw[(o * dim + c0 + c) * 9 + ky * 3 + kx] * v;
+                }
+    }
+    const int y = y0 + ly, x = x0 + lx;
+    if (y < oh && x < ow)
+        for (int o = 0; o < cout; ++o) out[(long(o) * oh + y) * ow + x] = acc[o];
+}
+
+bool tail_conv(const float* in, int dim, int H, int W, const float* w, int cout, float* out, int oh,
+               int ow, hipStream_t s) {
+    if (cout > 4 || dim > 64 || dim % 16 != 0) return false;
+    unsigned tiles = unsigned(((W + 15) / 16) * ((H + 15) / 16));
+    hipLaunchKernelGGL(k_tail, dim3(tiles), dim3(256), 0, s, in, dim, H, W, w, cout, out, oh, ow);
+    return true;
+}
+
+// ---------------------------------------------------------------------------
+// Layout changes: 32x32 tiles through LDS.
+// ---------------------------------------------------------------------------
+__global__ void k_nchw_to_nhwc(const float* __restrict__ src, float* __restrict__ dst, int c, long P, long ld) {
+    __shared__ float t[32][33];
+    long p0 = long(blockIdx.x) * 32;
+    int c0 = blockIdx.y * 32;
+    int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;   // 256 threads: 8 rows of 32
+    for (int i = ty; i < 32; i += 8) {
+        int cc = c0 + i;
+        long p = p0 + tx;
+        t[i][tx] = (cc < c && p < P) ? src[long(cc) * P + p] : 0.f;
+    }
+    __syncthreads();
+    for (int i = ty; i < 32; i += 8) {
+        long p = p0 + i;
+        int cc = c0 + tx;
+        if (cc < c && p < P) dst[p * ld + cc] = t[tx][i];
+    }
+}
+
+__global__ void k_nhwc_to_nchw(const float* __restrict__ src, float* __restrict__ dst, int c, long P, long ld) {
+    __shared__ float t[32][33];
+    long p0 = long(blockIdx.x) * 32;
+    int c0 = blockIdx.y * 32;
+    int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+    for (int i = ty; i < 32; i += 8) {
+        long p = p0 + i;
+        int cc = c0 + tx;
+        t[i][tx] = (cc < c && p < P) ? src[p * ld + cc] : 0.f;
+    }
+    __syncthreads();
+    for (int i = ty; i < 32; i += 8) {
+        int cc = c0 + i;
+        long p = p0 + tx;
+        if (cc < c && p < P) dst[long(cc) * P + p] = t[tx][i];
+    }
+}
+
+void nchw_to_nhwc(const float* src, float* dst, int c, long P, long ld, hipStream_t s) {
+    dim3 grid(unsigned((P + 31) / 32), unsigned((c + 31) / 32));
+    hipLaunchKernelGGL(k_nchw_to_nhwc, grid, dim3(256), 0, s, src, dst, c, P, ld);
+}
+void nhwc_to_nchw(const float* src, float* dst, int c, long P, long ld, hipStream_t s) {
+    dim3 grid(unsigned((P + 31) / 32), unsigned((c + 31) / 32));
+    hipLaunchKernelGGL(k_nhwc_to_nchw, grid, dim3(256), 0, s, src, dst, c, P, ld);
+}
+
+// The window map of the attention kernel (win_row, pixel mode), as a copy.
+__global__ void k_window_map(const float* __restrict__ src, float* __restrict__ dst, int c, int H, int W,
+                             int shift, int gather, long total) {
+    long gid = long(blockIdx.x) * 256 + threadIdx.x;
+    if (gid >= total) return;
+    int ch = int(gid % c);
+    long tokn = gid / c;
+    long wi = tokn >> 6;
+    int t = int(tokn & 63);
+    int nww = W / 8;
+    int wh = int(wi / nww), ww = int(wi % nww);
+    int y = wh * 8 + (t >> 3) + shift, x = ww * 8 + (t & 7) + shift;
+    if (y >= H) y -= H;
+    if (x >= W) x -= W;
+    long p = long(y) * W + x;
+    if (gather) dst[tokn * c + ch] = src[p * c + ch];
+    else dst[p * c + ch] = src[tokn * c + ch];
+}
+
+void window_gather(const float* x, float* tok, int c, int H, int W, int shift, hipStream_t s) {
+    long total = long(H) * W * c;
+    hipLaunchKernelGGL(k_window_map, dim3(unsigned((total + 255) / 256)), dim3(256), 0, s, x, tok, c, H, W,
+                       shift, 1, total);
+}
+void window_scatter(const float* tok, float* x, int c, int H, int W, int shift, hipStream_t s) {
+    long total = long(H) * W * c;
+    hipLaunchKernelGGL(k_window_map, dim3(unsigned((total + 255) / 256)), dim3(256), 0, s, tok, x, c, H, W,
+                       shift, 0, total);
+}
+
+}  // namespace scunet

@@ -1,0 +1,114 @@
+"""The drop-in boundary on the CPU: the library builds and exports exactly what the header
+declares, weight files are validated like src/weights.rs does, the plan geometry, and
+the product path never reaches the oracle."""
+import ctypes
+import os
+import re
+import subprocess
+
+import numpy as np
+import pytest
+
+REPO = os.path.abspath(os.path.join(os.path.dirname(__file__), ".."))
+HEADER = os.path.join(REPO, "include", "scunet_hip.h")
+PKG = os.path.join(REPO, "scunet-rs_amd")
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"\b(scunet_hip_\w+)\s*\(", text)))
+
+
+def test_header_and_python_binding_agree():
+    from scunet_hip import EXPORTS
+    assert sorted(EXPORTS) == declared_symbols()
+
+
+def test_library_exports_every_declared_symbol():
+    from scunet_hip import LIB_PATH
+    if not os.path.exists(LIB_PATH):
+        pytest.skip("library not built")
+    out = subprocess.run(["nm", "-D", "--defined-only", LIB_PATH], capture_output=True, text=True).stdout
+    exported = set(re.findall(r"\bT (scunet_hip_\w+)", out))
+    missing = [s for s in declared_symbols() if s not in exported]
+    assert not missing, missing
+    lib = ctypes.CDLL(LIB_PATH)          # loads without a GPU: no device call at load time
+    for s in declared_symbols():
+        assert hasattr(lib, s)
+
+
+def _write_bad(path, mutate):
+    from scunet_hip.safetensors_io import read_safetensors, write_safetensors
+    from scunet_hip import synth
+    t, meta = read_safetensors(synth.weights_file(seed=0))
+    t = {k: np.array(v) for k, v in t.items()}
+    mutate(t, meta)
+    write_safetensors(path, t, meta)
+
+
+@pytest.mark.parametrize("mutate,msg", [
+    (lambda t, m: m.pop("window_size"), "no `window_size` in __metadata__"),
+    (lambda t, m: m.__setitem__("arch", "swin2sr"), "not `scunet`"),
+    (lambda t, m: m.__setitem__("variant", "color-99"), "not one of the eight published"),
+    (lambda t, m: m.__setitem__("in_nc", "1"), "implies in_nc 3"),
+    (lambda t, m: m.__setitem__("config", "4,4,4"), "config has 3 entries"),
+    (lambda t, m: t.__setitem__("m_body.2.conv_block.0.weight", np.zeros((256, 256, 3, 1), np.float32)),
+     "m_body.2.conv_block.0.weight is [256, 256, 3, 1]"),
+    (lambda t, m: t.pop("m_up2.3.trans_block.ln2.bias"), "m_up2.3.trans_block.ln2.bias"),
+])
+def test_create_validates_the_checkpoint_like_weights_rs(tmp_path, mutate, msg):
+    """weights.rs:101-280: a malformed checkpoint fails at create with a message naming the
+    field, before any device is touched (so this runs without a GPU)."""
+    from scunet_hip import Hip, BackendError, LIB_PATH
+    if not os.path.exists(LIB_PATH):
+        pytest.skip("library not built")
+    p = str(tmp_path / "bad.safetensors")
+    _write_bad(p, mutate)
+    with pytest.raises(BackendError) as e:
+        Hip(p)
+    assert msg in str(e.value)
+
+
+def test_create_reports_a_missing_file():
+    from scunet_hip import Hip, BackendError, LIB_PATH
+    if not os.path.exists(LIB_PATH):
+        pytest.skip("library not built")
+    with pytest.raises(BackendError, match="No such file"):
+        Hip("/nonexistent/x.safetensors")
+
+
+def test_plan_geometry_and_min_size():
+    # plan.rs:43-57, parity.rs:129-141.
+    from scunet_hip import Plan, check_min_size, BackendError
+    p = Plan(80, 64)
+    assert (p.hp, p.wp) == (128, 64)
+    assert Plan(256, 256).hp == 256
+    assert Plan(257, 1).hp == 320
+    assert Plan(1080, 1920).windows(0) == (136, 240)
+    assert Plan(1080, 1920).windows(3) == (17, 30)
+    check_min_size(1, 1, 8)
+    with pytest.raises(BackendError):
+        check_min_size(1, 1, 16)
+
+
+def test_weights_generator_is_deterministic_and_loadable():
+    from scunet_hip import synth
+    from scunet_hip.safetensors_io import read_safetensors
+    a, meta = synth.make_weights(seed=11, in_nc=1, config=(2, 2, 2, 2, 2, 2, 2))
+    b, _ = synth.make_weights(seed=11, in_nc=1, config=(2, 2, 2, 2, 2, 2, 2))
+    assert all(np.array_equal(a[k], b[k]) for k in a)
+    assert meta["variant"].startswith("gray")
+    rp = a["m_down2.1.trans_block.msa.relative_position_params"]
+    assert rp.shape == (2, 15, 15) and np.abs(rp).max() <= 0.04
+    t, m = read_safetensors(synth.weights_file(seed=0))
+    assert m["arch"] == "scunet" and m["config"] == "4,4,4,4,4,4,4"
+    assert len(t) == len(synth.tensor_specs())
+
+
+def test_product_never_reaches_the_oracle():
+    """Only tests/, smoke() and bench.py's CPU baseline may touch oracle/."""
+    for root, _, files in os.walk(PKG):
+        for f in files:
+            if f.endswith((".py", ".hip", ".cpp", ".h", "Makefile")):
+                text = open(os.path.join(root, f), errors="replace").read()
+                assert "oracle" not in text.lower(), os.path.join(root, f)
