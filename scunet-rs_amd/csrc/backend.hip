@@ -231,19 +231,18 @@ bool run_conv3(scunet_hip* h, const Conv3Args& c, bool relu) {
 }
 
 // Scratch of one ConvTransBlock at width t on P pixels: y [P][2t], s1 [P][t],
-// qkv [P][3t], o [P][t], hid [P][4t].
+// qkv [P][3t], o [P][t].
 struct BlockScratch {
-    float *y, *s1, *qkv, *o, *hid;
+    float *y, *s1, *qkv, *o;
 };
 
 bool block_scratch(scunet_hip* h, long P, int t, BlockScratch* s) {
-    float* b = buf(h, "block", size_t(P) * 11 * t);
+    float* b = buf(h, "block", size_t(P) * 7 * t);
     if (!b) return false;
     s->y = b;
     s->s1 = s->y + size_t(P) * 2 * t;
     s->qkv = s->s1 + size_t(P) * t;
     s->o = s->qkv + size_t(P) * 3 * t;
-    s->hid = s->o + size_t(P) * t;
     return true;
 }
 
@@ -292,15 +291,16 @@ bool block(scunet_hip* h, const std::string& p, float* x, int H, int Wd, int shi
     g.A = s.o; g.lda = t; g.W = W(h, tp + ".msa.linear.weight"); g.bias = W(h, tp + ".msa.linear.bias");
     g.C = yt; g.ldc = c; g.R = yt; g.ldr = c; g.M = P; g.N = t; g.K = t;
     if (!run_gemm(h, "proj", g, A_ROWS, E_RESID)) return false;
-    g = GemmArgs{};
-    g.A = yt; g.lda = c; g.ln_g = W(h, tp + ".ln2.weight"); g.ln_b = W(h, tp + ".ln2.bias");
-    g.W = W(h, tp + ".mlp.0.weight"); g.bias = W(h, tp + ".mlp.0.bias");
-    g.C = s.hid; g.ldc = 4 * t; g.M = P; g.N = 4 * t; g.K = t;
-    if (!run_gemm(h, "mlp0_ln_gelu", g, A_LN, E_GELU)) return false;
-    g = GemmArgs{};
-    g.A = s.hid; g.lda = 4 * t; g.W = W(h, tp + ".mlp.2.weight"); g.bias = W(h, tp + ".mlp.2.bias");
-    g.C = yt; g.ldc = c; g.R = yt; g.ldr = c; g.M = P; g.N = t; g.K = 4 * t;
-    if (!run_gemm(h, "mlp2", g, A_ROWS, E_RESID)) return false;
+    {
+        MlpArgs m;
+        m.x = yt; m.ldx = c; m.ln_g = W(h, tp + ".ln2.weight"); m.ln_b = W(h, tp + ".ln2.bias");
+        m.w0 = W(h, tp + ".mlp.0.weight"); m.b0 = W(h, tp + ".mlp.0.bias");
+        m.w2 = W(h, tp + ".mlp.2.weight"); m.b2 = W(h, tp + ".mlp.2.bias"); m.M = P; m.t = t;
+        Span sp(h, "mlp_fused", 16.0 * double(P) * t * t, 4.0 * (2.0 * P * t + 8.0 * t * t + 5.0 * t));
+        const char* why = nullptr;
+        if (!mlp(m, h->stream, &why)) return fail(h, why);
+        if (!launched(h, "mlp")) return false;
+    }
     // conv1_2 on the concatenation, residual over the block: x += y W^T + b.
     g = GemmArgs{};
     g.A = s.y; g.lda = c; g.W = W(h, p + ".conv1_2.weight"); g.bias = W(h, p + ".conv1_2.bias");

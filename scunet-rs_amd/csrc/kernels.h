@@ -52,6 +52,23 @@ struct GemmArgs {
 // Returns false (and a reason) if no tile configuration fits the shape.
 bool gemm(const GemmArgs& g, GemmA a, GemmE e, hipStream_t s, const char** why);
 
+// The transformer half's MLP with its pre-norm and residual, fused (cpu.rs:800-860):
+// x[m] += W2 gelu(W0 LN(x[m]) + b0) + b2 for each row m of a [M][ldx] plane with t = T
+// columns. The 4t-wide hidden layer never leaves the CU.
+struct MlpArgs {
+    float* x = nullptr;
+    long ldx = 0;
+    const float* ln_g = nullptr;
+    const float* ln_b = nullptr;
+    const float* w0 = nullptr;     // [4t][t]
+    const float* b0 = nullptr;     // [4t]
+    const float* w2 = nullptr;     // [t][4t]
+    const float* b2 = nullptr;     // [t]
+    long M = 0;
+    int t = 0;
+};
+bool mlp(const MlpArgs& a, hipStream_t s, const char** why);
+
 struct Conv3Args {
     const float* in = nullptr;
     long ldi = 0;                  // channels [0, cin) of a [P][ldi] plane

@@ -271,6 +271,173 @@ bool gemm(const GemmArgs& g, GemmA a, GemmE e, hipStream_t s, const char** why) 
 }
 
 // ---------------------------------------------------------------------------
+// Fused MLP: x += W2 gelu(W0 LN(x) + b0) + b2, t = T channels, hidden 4T.
+// Each wave owns 16*MT rows; LN runs on the rows in registers (the 4 lanes 16 apart hold
+// one row between them). The hidden layer is produced HC units at a time and TRANSPOSED
+// (H^T = W0c Xn^T, hidden units as the MFMA M rows), which leaves each lane holding
+// H[row li][4 consecutive hidden units]: exactly the A operand of the second product, so
+// the hidden never goes through LDS or HBM. W0/W2 slices are double-buffered in LDS.
+// ---------------------------------------------------------------------------
+template <int T, int MT, int HC>
+__global__ __launch_bounds__(256) void k_mlp(MlpArgs a) {
+    constexpr int KG = T / 16, NT = T / 16, HT = HC / 16, NCH = 4 * T / HC;
+    constexpr int L0 = T + 4, L2 = HC + 4;
+    constexpr int BUF = HC * L0 + T * L2;
+    constexpr int W0V = HC * T / 4;               // float4 in a W0 slice
+    constexpr int PV = (2 * W0V) / 256;           // float4 per thread per slice (W0 then W2)
+    static_assert((2 * W0V) % 256 == 0 && W0V % 256 == 0, "slice must split evenly");
+    __shared__ float lds[2 * BUF];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int li = lane & 15, lg = lane >> 4;
+    const long row0 = long(blockIdx.x) * (64 * MT) + wave * 16 * MT;
+
+    f4 xa[MT][KG];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+        const long r = row0 + mt * 16 + li;
+#pragma unroll
+        for (int kg = 0; kg < KG; ++kg)
+            xa[mt][kg] = r < a.M ? ld4(a.x + r * a.ldx + kg * 16 + lg * 4) : f4{0.f, 0.f, 0.f, 0.f};
+    }
+    // LayerNorm, two-pass (cpu.rs:338-357).
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+        float s = 0.f;
+#pragma unroll
+        for (int kg = 0; kg < KG; ++kg) s += (xa[mt][kg].x + xa[mt][kg].y) + (xa[mt][kg].z + xa[mt][kg].w);
+        s += __shfl_xor(s, 16);
+        s += __shfl_xor(s, 32);
+        const float mu = s / float(T);
+        float q = 0.f;
+#pragma unroll
+        for (int kg = 0; kg < KG; ++kg) {
+            f4 d = xa[mt][kg] - mu;
+            q += (d.x * d.x + d.y * d.y) + (d.z * d.z + d.w * d.w);
+        }
+        q += __shfl_xor(q, 16);
+        q += __shfl_xor(q, 32);
+        const float rs = 1.0f / sqrtf(q / float(T) + 1e-5f);
+#pragma unroll
+        for (int kg = 0; kg < KG; ++kg) {
+            f4 g = ld4(a.ln_g + kg * 16 + lg * 4), b = ld4(a.ln_b + kg * 16 + lg * 4);
+            xa[mt][kg] = (xa[mt][kg] - mu) * rs * g + b;
+        }
+    }
+
+    f4 pre[PV];
+    auto gload = [&](int ch) {
+#pragma unroll
+        for (int i = 0; i < PV; ++i) {
+            const int f = tid + i * 256;
+            if (f < W0V) {
+                const int row = f / (T / 4), c4 = f % (T / 4);
+                pre[i] = ld4(a.w0 + long(ch * HC + row) * T + c4 * 4);
+            } else {
+                const int f2 = f - W0V;
+                const int row = f2 / (HC / 4), c4 = f2 % (HC / 4);
+                pre[i] = ld4(a.w2 + long(row) * (4 * T) + ch * HC + c4 * 4);
+            }
+        }
+    };
+    auto lstore = [&](int b) {
+        float* base = lds + b * BUF;
+#pragma unroll
+        for (int i = 0; i < PV; ++i) {
+            const int f = tid + i * 256;
+            if (f < W0V) {
+                const int row = f / (T / 4), c4 = f % (T / 4);
+                st4(base + row * L0 + c4 * 4, pre[i]);
+            } else {
+                const int f2 = f - W0V;
+                const int row = f2 / (HC / 4), c4 = f2 % (HC / 4);
+                st4(base + HC * L0 + row * L2 + c4 * 4, pre[i]);
+            }
+        }
+    };
+
+    f4 acc2[MT][NT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) acc2[mt][nt] = f4{0.f, 0.f, 0.f, 0.f};
+
+    gload(0);
+    lstore(0);
+    __syncthreads();
+    for (int ch = 0; ch < NCH; ++ch) {
+        const float* cur = lds + (ch & 1) * BUF;
+        if (ch + 1 < NCH) gload(ch + 1);
+        f4 acc1[HT][MT];
+#pragma unroll
+        for (int ht = 0; ht < HT; ++ht)
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) acc1[ht][mt] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kg = 0; kg < KG; ++kg)
+#pragma unroll
+            for (int ht = 0; ht < HT; ++ht) {
+                const f4 wv = ld4(cur + (ht * 16 + li) * L0 + kg * 16 + lg * 4);
+#pragma unroll
+                for (int s = 0; s < 4; ++s)
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt) acc1[ht][mt] = mfma4(wv[s], xa[mt][kg][s], acc1[ht][mt]);
+            }
+#pragma unroll
+        for (int ht = 0; ht < HT; ++ht) {
+            const f4 bb = ld4(a.b0 + ch * HC + ht * 16 + lg * 4);
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) acc1[ht][mt][r] = gelu_as(acc1[ht][mt][r] + bb[r]);
+        }
+#pragma unroll
+        for (int ht = 0; ht < HT; ++ht)
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+                const f4 wv = ld4(cur + HC * L0 + (nt * 16 + li) * L2 + ht * 16 + lg * 4);
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt) acc2[mt][nt] = mfma4(acc1[ht][mt][r], wv[r], acc2[mt][nt]);
+            }
+        if (ch + 1 < NCH) lstore((ch + 1) & 1);
+        __syncthreads();
+    }
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+        const float bv = a.b2[nt * 16 + li];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const long row = row0 + mt * 16 + lg * 4 + r;
+                if (row < a.M) {
+                    float* o = a.x + row * a.ldx + nt * 16 + li;
+                    *o = *o + (acc2[mt][nt][r] + bv);
+                }
+            }
+    }
+}
+
+bool mlp(const MlpArgs& a, hipStream_t s, const char** why) {
+    if (a.M <= 0) return true;
+    auto go = [&](auto kern, int rows_per_block) {
+        dim3 grid{unsigned((a.M + rows_per_block - 1) / rows_per_block), 1u, 1u};
+        dim3 block{256u, 1u, 1u};
+        hipLaunchKernelGGL(kern, grid, block, 0, s, a);
+    };
+    switch (a.t) {
+        case 32: go(k_mlp<32, 4, 64>, 256); break;
+        case 64: go(k_mlp<64, 2, 64>, 128); break;
+        case 128: go(k_mlp<128, 1, 32>, 64); break;
+        case 256: go(k_mlp<256, 1, 16>, 64); break;
+        default: *why = "mlp: t must be 32, 64, 128 or 256"; return false;
+    }
+    return true;
+}
+
+// ---------------------------------------------------------------------------
 // 3x3 convolution, stride 1, zero padding 1, no bias, as an implicit GEMM:
 // M = a 16x16 tile of output pixels, N = BN output channels, K = 9 taps x cin.
 // Each 16-channel input slice of the tile's 18x18 halo and the matching weights go
