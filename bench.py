@@ -113,19 +113,40 @@ def main():
     mpx = h * w / dt / 1e6
     log(f"bench: {dt * 1e3:.2f} ms/step, {mpx:.2f} Mpx/s")
 
-    kernels = []
+    # Rows are per (kernel class, UNet level "@Lk"); aggregate per class for the roofline.
+    total_ms = max(sum(r[2] for r in rows), 1e-9)
+    classes = {}
     for name, n, ms, flop, byts in rows:
-        kernels.append(roofline_of(name, n, ms, flop, byts))
-        kernels[-1]["share"] = round(ms / max(sum(r[2] for r in rows), 1e-9), 4)
+        base = name.split("@")[0]
+        agg = classes.setdefault(base, [0, 0.0, 0.0, 0.0])
+        agg[0] += n
+        agg[1] += ms
+        agg[2] += flop
+        agg[3] += byts
+    kernels = []
+    for base, (n, ms, flop, byts) in sorted(classes.items(), key=lambda kv: -kv[1][1]):
+        k = roofline_of(base, n, ms, flop, byts)
+        k["share"] = round(ms / total_ms, 4)
+        k["levels"] = {}
+        for name, n2, ms2, flop2, byts2 in rows:
+            if name.split("@")[0] == base and "@" in name:
+                lv = roofline_of(name, n2, ms2, flop2, byts2)
+                k["levels"][name.split("@")[1]] = {"achieved": lv["achieved"], "unit": lv["unit"],
+                                                   "frac": lv["frac"], "avg_launch_ms": lv["avg_launch_ms"],
+                                                   "ms_per_step": round(ms2 / args.steps, 4)}
+        kernels.append(k)
     for k in kernels:
         log(f"  {k['kernel']:>14}: {k['launches']:5d} launches, {k['avg_launch_ms'] * 1e3:9.1f} us avg, "
             f"{k['achieved']:9.2f} {k['unit']} ({100 * k['frac']:.1f}% of {k['bound']}), share {100 * k['share']:.1f}%")
+        for lvl, v in sorted(k["levels"].items()):
+            log(f"  {'':>14}   {lvl}: {v['avg_launch_ms'] * 1e3:9.1f} us avg, {v['ms_per_step']:7.3f} ms/step, "
+                f"{v['achieved']:9.2f} {v['unit']} ({100 * v['frac']:.1f}%)")
     dominant = kernels[0] if kernels else None
     attn = next((k for k in kernels if k["kernel"] == "attention"), None)
     attn_tflops = None
     if attn:
-        r = next(r for r in rows if r[0] == "attention")
-        attn_tflops = round(r[3] / (r[2] * 1e-3) / 1e12, 3)
+        agg = classes["attention"]
+        attn_tflops = round(agg[2] / (agg[1] * 1e-3) / 1e12, 3)
 
     cpu = None
     if not args.no_cpu_baseline:

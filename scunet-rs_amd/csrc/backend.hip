@@ -57,6 +57,7 @@ struct scunet_hip {
     std::map<std::string, std::pair<float*, size_t>> arena;
 
     bool prof = false;
+    std::string tag;                     // appended to profiler class names ("@L0".."@L3")
     std::vector<ProfRec> recs;
     std::vector<hipEvent_t> ev_pool;
     size_t ev_used = 0;
@@ -115,10 +116,10 @@ float* buf(scunet_hip* h, const std::string& role, size_t floats) {
 // Profiling (cuda.rs:263-273): an event pair per launch when on.
 struct Span {
     scunet_hip* h;
-    const char* name;
+    std::string name;
     double flop, bytes;
     hipEvent_t e0 = nullptr;
-    Span(scunet_hip* hh, const char* n, double f, double b) : h(hh), name(n), flop(f), bytes(b) {
+    Span(scunet_hip* hh, const char* n, double f, double b) : h(hh), name(std::string(n) + hh->tag), flop(f), bytes(b) {
         if (!h->prof) return;
         e0 = next();
         hipEventRecord(e0, h->stream);
@@ -347,6 +348,7 @@ bool walk(scunet_hip* h, const float* x, int hh, int ww, int H, int Wd, float* y
             if (!skip[k]) return false;
         }
     }
+    h->tag.clear();
     {
         Span sp(h, "head", 2.0 * 9 * in_nc * dim * double(P[0]), 4.0 * (in_nc + dim) * double(P[0]));
         head_conv(x, in_nc, hh, ww, H, Wd, W(h, "m_head.0.weight"), dim, cur[0], false, h->stream);
@@ -357,6 +359,7 @@ bool walk(scunet_hip* h, const float* x, int hh, int ww, int H, int Wd, float* y
         const std::string name = STAGE[k];
         const int count = wt.config[k];
         const int c = dim << k;
+        h->tag = "@L" + std::to_string(k);
         for (int i = 0; i < count; ++i)
             if (!block(h, "m_" + name + "." + std::to_string(i), cur[k], Hs[k], Ws[k], (i & 1) ? wt.window / 2 : 0))
                 return false;
@@ -368,6 +371,7 @@ bool walk(scunet_hip* h, const float* x, int hh, int ww, int H, int Wd, float* y
         if (!run_gemm(h, "down2x2", g, A_S2D, E_DUAL)) return false;
         if (!dump_plane(h, hook, user, ("m_" + name).c_str(), skip[k + 1], 2 * c, P[k + 1])) return false;
     }
+    h->tag = "@L3";
     for (int i = 0; i < wt.config[3]; ++i)
         if (!block(h, "m_body." + std::to_string(i), cur[3], Hs[3], Ws[3], (i & 1) ? wt.window / 2 : 0))
             return false;
@@ -376,6 +380,7 @@ bool walk(scunet_hip* h, const float* x, int hh, int ww, int H, int Wd, float* y
         const std::string name = STAGE[4 + k];
         const int lvl = 2 - k;               // up3 -> level 2, up2 -> 1, up1 -> 0
         const int co = dim << lvl, ci = 2 * co;
+        h->tag = "@L" + std::to_string(lvl);
         GemmArgs g;
         g.A = cur[lvl + 1]; g.A2 = skip[lvl + 1]; g.lda = ci;
         g.W = W(h, "m_" + name + ".0.weight");
@@ -388,6 +393,7 @@ bool walk(scunet_hip* h, const float* x, int hh, int ww, int H, int Wd, float* y
                 return false;
         if (!dump_plane(h, hook, user, ("m_" + name).c_str(), cur[lvl], co, P[lvl])) return false;
     }
+    h->tag.clear();
     {
         Span sp(h, "head", 2.0 * 9 * in_nc * dim * double(P[0]), 4.0 * (in_nc + 2 * dim) * double(P[0]));
         head_conv(x, in_nc, hh, ww, H, Wd, W(h, "m_head.0.weight"), dim, cur[0], true, h->stream);

@@ -224,6 +224,237 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// GEMM, "A-direct" form: each wave owns 16*MT rows and all BN columns of its
+// workgroup and loads its A fragments straight from HBM into MFMA registers (a row's
+// 4 consecutive k values per lane, 64 contiguous bytes per row per instruction); only
+// the weight slice [BN][KC], shared by the 4 waves, goes through LDS, double-buffered.
+// The next A slice and the next weight slice are loaded while the current one is
+// multiplied. LN mode (KLN = K > 0) holds the whole row in registers, normalises it
+// there (two-pass, cpu.rs:338-357) and streams only the weights.
+// ---------------------------------------------------------------------------
+template <int MT, int BN, int KC, int AM, int EP, int KLN>
+__global__ __launch_bounds__(256) void k_gemm2(GemmArgs g) {
+    constexpr int NT = BN / 16, KG = KC / 16, LDB = KC + 4;
+    constexpr int BV = BN * KC / 4 / 256;
+    static_assert(BN * KC / 4 % 256 == 0, "weight slice must split evenly over 256 threads");
+    constexpr bool LN = AM == A_LN;
+    constexpr int XKG = LN ? KLN / 16 : 1;
+    __shared__ float Bs[2 * BN * LDB];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int li = lane & 15, lg = lane >> 4;
+    const int ntn = g.N / BN;
+    const long tile = xcd_swizzle(blockIdx.x, gridDim.x);
+    const long m0 = (tile / ntn) * (64 * MT) + wave * 16 * MT;
+    const int n0 = int(tile % ntn) * BN;
+
+    auto a_addr = [&](long row, int k) -> const float* {
+        if constexpr (AM == A_S2D) {
+            const int tap = k / g.cin, ci = k - tap * g.cin;
+            const int ow = g.in_w >> 1;
+            const long oy = row / ow, ox = row - oy * ow;
+            const long ip = (2 * oy + (tap >> 1)) * long(g.in_w) + 2 * ox + (tap & 1);
+            return g.A + ip * g.cin + ci;
+        } else {
+            return g.A + row * g.lda + k;
+        }
+    };
+    auto a_get = [&](long row, int k) -> f4 {
+        if (row >= g.M) return f4{0.f, 0.f, 0.f, 0.f};
+        if constexpr (AM == A_ADD2) return ld4(g.A + row * g.lda + k) + ld4(g.A2 + row * g.lda + k);
+        return ld4(a_addr(row, k));
+    };
+
+    f4 xl[LN ? MT : 1][XKG];
+    if constexpr (LN) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+            const long r = m0 + mt * 16 + li;
+#pragma unroll
+            for (int kg = 0; kg < XKG; ++kg) xl[mt][kg] = a_get(r, kg * 16 + lg * 4);
+            float sm = 0.f;
+#pragma unroll
+            for (int kg = 0; kg < XKG; ++kg) sm += (xl[mt][kg].x + xl[mt][kg].y) + (xl[mt][kg].z + xl[mt][kg].w);
+            sm += __shfl_xor(sm, 16);
+            sm += __shfl_xor(sm, 32);
+            const float mu = sm / float(KLN);
+            float q = 0.f;
+#pragma unroll
+            for (int kg = 0; kg < XKG; ++kg) {
+                f4 d = xl[mt][kg] - mu;
+                q += (d.x * d.x + d.y * d.y) + (d.z * d.z + d.w * d.w);
+            }
+            q += __shfl_xor(q, 16);
+            q += __shfl_xor(q, 32);
+            const float rs = 1.0f / sqrtf(q / float(KLN) + 1e-5f);
+#pragma unroll
+            for (int kg = 0; kg < XKG; ++kg) {
+                f4 gg = ld4(g.ln_g + kg * 16 + lg * 4), bb = ld4(g.ln_b + kg * 16 + lg * 4);
+                xl[mt][kg] = (xl[mt][kg] - mu) * rs * gg + bb;
+            }
+        }
+    }
+
+    f4 bpre[BV];
+    auto bload = [&](int k0) {
+#pragma unroll
+        for (int i = 0; i < BV; ++i) {
+            const int f = tid + i * 256;
+            const int row = f / (KC / 4), c4 = f % (KC / 4);
+            bpre[i] = ld4(g.W + long(n0 + row) * g.K + k0 + c4 * 4);
+        }
+    };
+    auto bstore = [&](int b) {
+#pragma unroll
+        for (int i = 0; i < BV; ++i) {
+            const int f = tid + i * 256;
+            const int row = f / (KC / 4), c4 = f % (KC / 4);
+            st4(&Bs[b * BN * LDB + row * LDB + c4 * 4], bpre[i]);
+        }
+    };
+    f4 acur[LN ? 1 : MT][LN ? 1 : KG], anext[LN ? 1 : MT][LN ? 1 : KG];
+    auto aload = [&](int k0, f4 (&dst)[LN ? 1 : MT][LN ? 1 : KG]) {
+        if constexpr (!LN) {
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int kg = 0; kg < KG; ++kg) dst[mt][kg] = a_get(m0 + mt * 16 + li, k0 + kg * 16 + lg * 4);
+        }
+    };
+
+    f4 acc[MT][NT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = f4{0.f, 0.f, 0.f, 0.f};
+
+    auto step = [&](int c, bool more) {
+        const float* B = Bs + (c & 1) * BN * LDB;
+#pragma unroll
+        for (int kg = 0; kg < KG; ++kg) {
+            f4 b[NT];
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) b[nt] = ld4(B + (nt * 16 + li) * LDB + kg * 16 + lg * 4);
+#pragma unroll
+            for (int s4 = 0; s4 < 4; ++s4)
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) {
+                    float av;
+                    if constexpr (LN) av = xl[mt][c * KG + kg][s4];
+                    else av = acur[mt][kg][s4];
+#pragma unroll
+                    for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = mfma4(b[nt][s4], av, acc[mt][nt]);
+                }
+        }
+        if (more) bstore((c + 1) & 1);
+        __syncthreads();
+    };
+
+    bload(0);
+    bstore(0);
+    aload(0, acur);
+    __syncthreads();
+    if constexpr (LN) {
+        constexpr int NCH = KLN / KC;
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+            if (c + 1 < NCH) bload((c + 1) * KC);
+            step(c, c + 1 < NCH);
+        }
+    } else {
+        const int nch = g.K / KC;
+        for (int c = 0; c < nch; ++c) {
+            const bool more = c + 1 < nch;
+            if (more) {
+                bload((c + 1) * KC);
+                aload((c + 1) * KC, anext);
+            }
+            step(c, more);
+            if (more) {
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                    for (int kg = 0; kg < KG; ++kg) acur[mt][kg] = anext[mt][kg];
+            }
+        }
+    }
+
+    // The product was computed transposed (weights as the M rows), so each lane holds 4
+    // consecutive output columns of one row: one 16-byte store per row and N tile.
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+        const int col = n0 + nt * 16 + lg * 4;
+        const f4 bv = g.bias ? ld4(g.bias + col) : f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+            const long row = m0 + mt * 16 + li;
+            if (row >= g.M) continue;
+            f4 v = acc[mt][nt] + bv;
+            if constexpr (EP == E_STORE) {
+                st4(g.C + row * g.ldc + col, v);
+            } else if constexpr (EP == E_DUAL) {
+                st4(g.C + row * g.ldc + col, v);
+                st4(g.C2 + row * g.ldc + col, v);
+            } else if constexpr (EP == E_GELU) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) v[r] = gelu_as(v[r]);
+                st4(g.C + row * g.ldc + col, v);
+            } else if constexpr (EP == E_RESID) {
+                st4(g.C + row * g.ldc + col, ld4(g.R + row * g.ldr + col) + v);
+            } else {
+                const long ii = row / g.in_w, jj = row - ii * g.in_w;
+                const int tap = col / g.cout, co = col - tap * g.cout;
+                const long oy = 2 * ii + (tap >> 1), ox = 2 * jj + (tap & 1);
+                st4(g.C + (oy * 2 * g.in_w + ox) * g.cout + co, v);
+            }
+        }
+    }
+}
+
+template <int MT, int BN, int KC, int AM, int KLN>
+static void launch_gemm2_e(const GemmArgs& g, GemmE e, hipStream_t s) {
+    const long tiles = ((g.M + 64 * MT - 1) / (64 * MT)) * (g.N / BN);
+    dim3 grid{unsigned(tiles), 1u, 1u}, block{256u, 1u, 1u};
+    switch (e) {
+        case E_STORE: hipLaunchKernelGGL((k_gemm2<MT, BN, KC, AM, E_STORE, KLN>), grid, block, 0, s, g); break;
+        case E_DUAL: hipLaunchKernelGGL((k_gemm2<MT, BN, KC, AM, E_DUAL, KLN>), grid, block, 0, s, g); break;
+        case E_GELU: hipLaunchKernelGGL((k_gemm2<MT, BN, KC, AM, E_GELU, KLN>), grid, block, 0, s, g); break;
+        case E_RESID: hipLaunchKernelGGL((k_gemm2<MT, BN, KC, AM, E_RESID, KLN>), grid, block, 0, s, g); break;
+        case E_D2S: hipLaunchKernelGGL((k_gemm2<MT, BN, KC, AM, E_D2S, KLN>), grid, block, 0, s, g); break;
+    }
+}
+
+template <int MT, int BN, int KC>
+static void launch_gemm2_a(const GemmArgs& g, GemmA a, GemmE e, hipStream_t s) {
+    switch (a) {
+        case A_ROWS: launch_gemm2_e<MT, BN, KC, A_ROWS, 0>(g, e, s); break;
+        case A_S2D: launch_gemm2_e<MT, BN, KC, A_S2D, 0>(g, e, s); break;
+        case A_ADD2: launch_gemm2_e<MT, BN, KC, A_ADD2, 0>(g, e, s); break;
+        default: break;
+    }
+}
+
+// Tile choice: the widest N block (<= 128) that divides N; 256 rows per workgroup for
+// N <= 64, 128 above; 32-wide K slices.
+static bool launch_gemm2(const GemmArgs& g, GemmA a, GemmE e, hipStream_t s) {
+    if (a == A_LN) {
+        switch (g.K) {
+            case 32: if (g.N % 96 == 0) { launch_gemm2_e<4, 96, 32, A_LN, 32>(g, e, s); return true; } break;
+            case 64: if (g.N % 96 == 0) { launch_gemm2_e<2, 96, 64, A_LN, 64>(g, e, s); return true; } break;
+            case 128: if (g.N % 128 == 0) { launch_gemm2_e<1, 128, 64, A_LN, 128>(g, e, s); return true; } break;
+            case 256: if (g.N % 128 == 0) { launch_gemm2_e<1, 128, 64, A_LN, 256>(g, e, s); return true; } break;
+        }
+        return false;
+    }
+    if (g.N % 128 == 0) launch_gemm2_a<2, 128, 32>(g, a, e, s);
+    else if (g.N % 96 == 0) launch_gemm2_a<2, 96, 32>(g, a, e, s);
+    else if (g.N % 64 == 0) launch_gemm2_a<4, 64, 32>(g, a, e, s);
+    else if (g.N % 32 == 0) launch_gemm2_a<4, 32, 32>(g, a, e, s);
+    else return false;
+    return true;
+}
+
 template <int BM, int BN, int WM, int WN, int AM>
 static void launch_gemm_e(const GemmArgs& g, GemmE e, hipStream_t s) {
     long tiles = ((g.M + BM - 1) / BM) * (g.N / BN);
@@ -262,6 +493,7 @@ bool gemm(const GemmArgs& g, GemmA a, GemmE e, hipStream_t s, const char** why) 
         *why = "gemm: depth-to-space needs cout % 16 == 0 and N == 4 cout";
         return false;
     }
+    if (launch_gemm2(g, a, e, s)) return true;
     if (g.N % 128 == 0) launch_gemm_a<128, 128, 64, 64>(g, a, e, s);
     else if (g.N % 96 == 0) launch_gemm_a<128, 96, 32, 96>(g, a, e, s);
     else if (g.N % 64 == 0) launch_gemm_a<256, 64, 64, 64>(g, a, e, s);
@@ -399,24 +631,23 @@ __global__ __launch_bounds__(256) void k_mlp(MlpArgs a) {
 #pragma unroll
                 for (int r = 0; r < 4; ++r)
 #pragma unroll
-                    for (int mt = 0; mt < MT; ++mt) acc2[mt][nt] = mfma4(acc1[ht][mt][r], wv[r], acc2[mt][nt]);
+                    for (int mt = 0; mt < MT; ++mt) acc2[mt][nt] = mfma4(wv[r], acc1[ht][mt][r], acc2[mt][nt]);
             }
         if (ch + 1 < NCH) lstore((ch + 1) & 1);
         __syncthreads();
     }
+    // out^T = W2 H^T: each lane holds 4 consecutive output channels of one row.
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
-        const float bv = a.b2[nt * 16 + li];
+        const f4 bv = ld4(a.b2 + nt * 16 + lg * 4);
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const long row = row0 + mt * 16 + lg * 4 + r;
-                if (row < a.M) {
-                    float* o = a.x + row * a.ldx + nt * 16 + li;
-                    *o = *o + (acc2[mt][nt][r] + bv);
-                }
+        for (int mt = 0; mt < MT; ++mt) {
+            const long row = row0 + mt * 16 + li;
+            if (row < a.M) {
+                float* o = a.x + row * a.ldx + nt * 16 + lg * 4;
+                st4(o, ld4(o) + (acc2[mt][nt] + bv));
             }
+        }
     }
 }
 
@@ -527,7 +758,7 @@ __global__ __launch_bounds__(256) void k_conv3x3(Conv3Args a) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
 #pragma unroll
-                    for (int j = 0; j < NT; ++j) acc[i][j] = mfma4(av[i][s], bv[j][s], acc[i][j]);
+                    for (int j = 0; j < NT; ++j) acc[i][j] = mfma4(bv[j][s], av[i][s], acc[i][j]);
         }
         __syncthreads();
         if (more) {
@@ -536,20 +767,23 @@ __global__ __launch_bounds__(256) void k_conv3x3(Conv3Args a) {
         }
     }
 
+    // Computed transposed (weights as the M rows): each lane holds output channels
+    // co0 + 16j + 4lg .. +3 of pixel (y0 + 4*wave + i, x0 + li).
+    const int x = x0 + li;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int y = y0 + wave * 4 + i;
-        if (y >= a.H) continue;
+        if (y >= a.H || x >= a.W) continue;
+        float* o = a.out + (long(y) * a.W + x) * a.ldo + co0 + lg * 4;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int x = x0 + lg * 4 + r;
-            if (x >= a.W) continue;
-            float* o = a.out + (long(y) * a.W + x) * a.ldo + co0 + li;
+        for (int j = 0; j < NT; ++j) {
+            f4 v = acc[i][j];
+            if constexpr (RELU) {
 #pragma unroll
-            for (int j = 0; j < NT; ++j) {
-                float v = acc[i][j][r];
-                if constexpr (RELU) o[j * 16] = fmaxf(v, 0.0f);
-                else o[j * 16] += v;
+                for (int r = 0; r < 4; ++r) v[r] = fmaxf(v[r], 0.0f);
+                st4(o + j * 16, v);
+            } else {
+                st4(o + j * 16, ld4(o + j * 16) + v);
             }
         }
     }
@@ -679,6 +913,9 @@ __global__ __launch_bounds__(256) void k_attention(AttnArgs a, long units) {
         sum += __shfl_xor(sum, 32);
         const float inv = 1.0f / sum;
 
+        // O^T = V^T P^T: the probabilities are the B operand as they stand (lane = query,
+        // registers = 4 consecutive keys), V the A operand; the result leaves each lane with
+        // 4 consecutive dims of one query: dims 16nd + 4lg .. +3 of query 16nt + li.
         f4 O[2] = {f4{0.f, 0.f, 0.f, 0.f}, f4{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
         for (int kt = 0; kt < 4; ++kt)
@@ -686,16 +923,11 @@ __global__ __launch_bounds__(256) void k_attention(AttnArgs a, long units) {
             for (int r = 0; r < 4; ++r) {
                 float p = S[kt][r] * inv;
 #pragma unroll
-                for (int nd = 0; nd < 2; ++nd) O[nd] = mfma4(p, vv[kt][r][nd], O[nd]);
+                for (int nd = 0; nd < 2; ++nd) O[nd] = mfma4(vv[kt][r][nd], p, O[nd]);
             }
-        // O lane layout: query 16nt + 4lg + r, dim 16nd + li.
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            long orow = win_row(a, wi, nt * 16 + lg * 4 + r, wh, ww);
-            float* o = a.out + orow * a.ldo + hoff + li;
-            o[0] = O[0][r];
-            o[16] = O[1][r];
-        }
+        float* o = a.out + qrow * a.ldo + hoff + lg * 4;
+        st4(o, O[0]);
+        st4(o + 16, O[1]);
     }
 }
 
