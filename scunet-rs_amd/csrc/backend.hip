@@ -351,7 +351,8 @@ bool walk(scunet_hip* h, const float* x, int hh, int ww, int H, int Wd, float* y
     h->tag.clear();
     {
         Span sp(h, "head", 2.0 * 9 * in_nc * dim * double(P[0]), 4.0 * (in_nc + dim) * double(P[0]));
-        head_conv(x, in_nc, hh, ww, H, Wd, W(h, "m_head.0.weight"), dim, cur[0], false, h->stream);
+        if (!head_conv(x, in_nc, hh, ww, H, Wd, W(h, "m_head.0.weight"), dim, cur[0], false, h->stream))
+            return fail(h, "m_head: unsupported shape");
         if (!launched(h, "m_head")) return false;
     }
     if (!dump_plane(h, hook, user, "m_head", cur[0], dim, P[0])) return false;
@@ -396,7 +397,8 @@ bool walk(scunet_hip* h, const float* x, int hh, int ww, int H, int Wd, float* y
     h->tag.clear();
     {
         Span sp(h, "head", 2.0 * 9 * in_nc * dim * double(P[0]), 4.0 * (in_nc + 2 * dim) * double(P[0]));
-        head_conv(x, in_nc, hh, ww, H, Wd, W(h, "m_head.0.weight"), dim, cur[0], true, h->stream);
+        if (!head_conv(x, in_nc, hh, ww, H, Wd, W(h, "m_head.0.weight"), dim, cur[0], true, h->stream))
+            return fail(h, "m_head: unsupported shape");
         if (!launched(h, "m_head (tail input)")) return false;
     }
     if (!dump_plane(h, hook, user, "m_tail_in", cur[0], dim, P[0])) return false;
@@ -717,7 +719,8 @@ int scunet_hip_op_probe(scunet_hip* h, const char* op, const char* name, const f
         float* yo = buf(h, "probe_out", c_out * size_t(Po));
         if (!yt || !yo) return false;
         if (o == "conv3x3" && n == "m_head.0") {
-            head_conv(dx, int(c_in), int(hh), int(ww), int(hh), int(ww), wp, int(c_out), yt, false, h->stream);
+            if (!head_conv(dx, int(c_in), int(hh), int(ww), int(hh), int(ww), wp, int(c_out), yt, false, h->stream))
+                return fail(h, "m_head: unsupported shape");
         } else if (o == "conv3x3" && n == "m_tail.0") {
             nchw_to_nhwc(dx, xt, int(c_in), P, long(c_in), h->stream);
             if (!tail_conv(xt, int(c_in), int(hh), int(ww), wp, int(c_out), yo, int(hh), int(ww), h->stream))

@@ -956,102 +956,131 @@ void build_bias_table(const float* rp, int heads, float* tab) {
 }
 
 // ---------------------------------------------------------------------------
-// m_head: in_nc -> dim 3x3 from the NCHW image, replicate padding to H x W folded into
-// the reads (plan.rs:67-82) and zero padding outside the plane (cpu.rs:66-71). Terms
-// are added channel, ky, kx ascending with separate multiply and add, as cpu.rs:99-127
-// does, so this stage reproduces the reference bit for bit.
+// m_head: in_nc -> 64, 3x3, as a small implicit GEMM on the matrix cores. K = in_nc*9
+// (channel, ky, kx) padded to 32; out^T = W A^T so each lane ends with 4 consecutive
+// output channels of one pixel. The input is the NCHW image of size hh x ww, replicate-
+// padded on the fly to the H x W plane (plan.rs:67-82) and zero-padded outside it
+// (cpu.rs:66-71). Each wave computes 16 pixels x 64 channels per step, 4 steps.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void k_head(const float* __restrict__ x, int cin, int hh, int ww,
-                                              int H, int W, const float* __restrict__ w, int dim,
-                                              float* __restrict__ out, int add, long total) {
-#pragma clang fp contract(off)
-    extern __shared__ float sw[];
-    for (int i = threadIdx.x; i < dim * cin * 9; i += 256) sw[i] = w[i];
+__global__ __launch_bounds__(256) void k_head(const float* __restrict__ x, int cin, int hh, int ww, int H,
+                                              int W, const float* __restrict__ w, float* __restrict__ out,
+                                              int add, long P) {
+    constexpr int LDW = 36;
+    __shared__ float sw[64 * LDW];            // W[co][k], k = ci*9 + tap, zero beyond cin*9
+    const int K = cin * 9;
+    for (int i = threadIdx.x; i < 64 * 32; i += 256) {
+        const int co = i >> 5, k = i & 31;
+        sw[co * LDW + k] = k < K ? w[co * K + k] : 0.0f;
+    }
     __syncthreads();
-    const int groups = dim >> 2;
-    long gid = long(blockIdx.x) * 256 + threadIdx.x;
-    if (gid >= total) return;
-    long p = gid / groups;
-    int cg = int(gid - p * groups);
-    int y = int(p / W), xx = int(p - long(y) * W);
-    float acc[4] = {0.f, 0.f, 0.f, 0.f};
-    for (int ci = 0; ci < cin; ++ci) {
-        const float* plane = x + long(ci) * hh * ww;
-        for (int ky = 0; ky < 3; ++ky) {
-            int sy = y + ky - 1;
-            if (sy < 0 || sy >= H) continue;
-            int cy = sy < hh ? sy : hh - 1;
-            for (int kx = 0; kx < 3; ++kx) {
-                int sx = xx + kx - 1;
-                if (sx < 0 || sx >= W) continue;
-                int cx = sx < ww ? sx : ww - 1;
-                float v = plane[long(cy) * ww + cx];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int li = lane & 15, lg = lane >> 4;
+    f4 wf[4][2];
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    float k = sw[((cg * 4 + j) * cin + ci) * 9 + ky * 3 + kx];
-                    acc[j] = acc[j] + k * v;   // contraction is off: a multiply, then an add
+    for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+        for (int kg = 0; kg < 2; ++kg) wf[nt][kg] = ld4(&sw[(nt * 16 + li) * LDW + kg * 16 + lg * 4]);
+    for (int step = 0; step < 4; ++step) {
+        const long p = (long(blockIdx.x) * 16 + wave * 4 + step) * 16 + li;
+        const int y = int(p / W), xx = int(p - long(y) * W);
+        f4 av[2];
+#pragma unroll
+        for (int kg = 0; kg < 2; ++kg)
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                const int k = kg * 16 + lg * 4 + s;
+                float v = 0.0f;
+                if (k < K && p < P) {
+                    const int ci = k / 9, tap = k - ci * 9;
+                    const int sy = y + tap / 3 - 1, sx = xx + tap % 3 - 1;
+                    if (sy >= 0 && sy < H && sx >= 0 && sx < W)
+                        v = x[(long(ci) * hh + (sy < hh ? sy : hh - 1)) * ww + (sx < ww ? sx : ww - 1)];
                 }
+                av[kg][s] = v;
             }
+        f4 acc[4];
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) acc[nt] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kg = 0; kg < 2; ++kg)
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
+#pragma unroll
+                for (int nt = 0; nt < 4; ++nt) acc[nt] = mfma4(wf[nt][kg][s], av[kg][s], acc[nt]);
+        if (p < P) {
+            float* o = out + p * 64 + lg * 4;
+#pragma unroll
+            for (int nt = 0; nt < 4; ++nt) st4(o + nt * 16, add ? ld4(o + nt * 16) + acc[nt] : acc[nt]);
         }
     }
-    float* o = out + p * dim + cg * 4;
-    f4 r = {acc[0], acc[1], acc[2], acc[3]};
-    if (add) r = ld4(o) + r;
-    st4(o, r);
 }
 
 bool head_conv(const float* x, int cin, int hh, int ww, int H, int W, const float* w, int dim,
                float* out, bool add, hipStream_t s) {
-    long total = long(H) * W * (dim / 4);
-    size_t shm = size_t(dim) * cin * 9 * sizeof(float);
-    hipLaunchKernelGGL(k_head, dim3(unsigned((total + 255) / 256)), dim3(256), shm, s, x, cin, hh, ww,
-                       H, W, w, dim, out, add ? 1 : 0, total);
+    if (dim != 64 || cin * 9 > 32) return false;
+    const long P = long(H) * W;
+    hipLaunchKernelGGL(k_head, dim3(unsigned((P + 255) / 256)), dim3(256), 0, s, x, cin, hh, ww, H, W, w, out,
+                       add ? 1 : 0, P);
     return true;
 }
 
 // ---------------------------------------------------------------------------
-// m_tail: dim -> cout 3x3 from the pixel-major plane into NCHW, cropped to oh x ow.
-// A 16x16 output tile; 16-channel slices of the 18x18 halo go through LDS; one thread
-// per output pixel accumulates all cout (<= 4) outputs, channel, ky, kx ascending.
+// m_tail: 64 -> cout (1 or 3), 3x3, from the pixel-major plane into NCHW, cropped to
+// oh x ow (plan.rs:85-94). One thread per output pixel of a 16x16 tile; 16-channel slices
+// of the 18x18 halo go through LDS as float4; the weights are wave-uniform, so they are
+// read through the scalar cache and used as scalar operands of the FMAs.
+// Sum order per output: channel, ky, kx ascending (cpu.rs:99-127).
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void k_tail(const float* __restrict__ in, int dim, int H, int W,
-                                              const float* __restrict__ w, int cout, float* __restrict__ out,
-                                              int oh, int ow) {
-    constexpr int HW = 18, CH = 16, LDC = CH + 1;
+template <int COUT>
+__global__ __launch_bounds__(256) void k_tail(const float* __restrict__ in, int H, int W,
+                                              const float* __restrict__ w, float* __restrict__ out, int oh,
+                                              int ow) {
+    constexpr int HW = 18, CH = 16, LDC = CH + 4, DIM = 64;
     __shared__ float hs[HW * HW * LDC];
-    __shared__ float sw[4 * 64 * 9];
-    for (int i = threadIdx.x; i < cout * dim * 9; i += 256) sw[i] = w[i];
     const int tx = (W + 15) / 16;
     const int y0 = int(blockIdx.x / tx) * 16, x0 = int(blockIdx.x % tx) * 16;
     const int ly = threadIdx.x >> 4, lx = threadIdx.x & 15;
-    float acc[4] = {0.f, 0.f, 0.f, 0.f};
-    for (int c0 = 0; c0 < dim; c0 += CH) {
+    float acc[COUT];
+#pragma unroll
+    for (int o = 0; o < COUT; ++o) acc[o] = 0.f;
+    for (int c0 = 0; c0 < DIM; c0 += CH) {
         __syncthreads();
-        for (int f = threadIdx.x; f < HW * HW * CH; f += 256) {
-            int px = f / CH, c = f % CH;
-            int gy = y0 - 1 + px / HW, gx = x0 - 1 + px % HW;
-            float v = 0.f;
-            if (gy >= 0 && gy < H && gx >= 0 && gx < W) v = in[(long(gy) * W + gx) * dim + c0 + c];
-            hs[px * LDC + c] = v;
+        for (int f = threadIdx.x; f < HW * HW * 4; f += 256) {
+            const int px = f >> 2, c4 = f & 3;
+            const int gy = y0 - 1 + px / HW, gx = x0 - 1 + px % HW;
+            f4 v = {0.f, 0.f, 0.f, 0.f};
+            if (gy >= 0 && gy < H && gx >= 0 && gx < W) v = ld4(in + (long(gy) * W + gx) * DIM + c0 + c4 * 4);
+            st4(&hs[px * LDC + c4 * 4], v);
         }
         __syncthreads();
-        for (int c = 0; c < CH; ++c)
-            for (int ky = 0; ky < 3; ++ky)
-                for (int kx = 0; kx < 3; ++kx) {
-                    float v = hs[((ly + ky) * HW + lx + kx) * LDC + c];
-                    for (int o = 0; o < cout; ++o) acc[o] += sw[(o * dim + c0 + c) * 9 + ky * 3 + kx] * v;
-                }
+#pragma unroll
+        for (int c4 = 0; c4 < 4; ++c4) {
+            f4 v[9];
+#pragma unroll
+            for (int tap = 0; tap < 9; ++tap) v[tap] = ld4(&hs[((ly + tap / 3) * HW + lx + tap % 3) * LDC + c4 * 4]);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int c = c0 + c4 * 4 + e;
+#pragma unroll
+                for (int tap = 0; tap < 9; ++tap)
+#pragma unroll
+                    for (int o = 0; o < COUT; ++o) acc[o] += w[(o * DIM + c) * 9 + tap] * v[tap][e];
+            }
+        }
     }
     const int y = y0 + ly, x = x0 + lx;
     if (y < oh && x < ow)
-        for (int o = 0; o < cout; ++o) out[(long(o) * oh + y) * ow + x] = acc[o];
+#pragma unroll
+        for (int o = 0; o < COUT; ++o) out[(long(o) * oh + y) * ow + x] = acc[o];
 }
 
 bool tail_conv(const float* in, int dim, int H, int W, const float* w, int cout, float* out, int oh,
                int ow, hipStream_t s) {
-    if (cout > 4 || dim > 64 || dim % 16 != 0) return false;
-    unsigned tiles = unsigned(((W + 15) / 16) * ((H + 15) / 16));
-    hipLaunchKernelGGL(k_tail, dim3(tiles), dim3(256), 0, s, in, dim, H, W, w, cout, out, oh, ow);
+    if (dim != 64) return false;
+    const unsigned tiles = unsigned(((W + 15) / 16) * ((H + 15) / 16));
+    if (cout == 3) hipLaunchKernelGGL(k_tail<3>, dim3(tiles), dim3(256), 0, s, in, H, W, w, out, oh, ow);
+    else if (cout == 1) hipLaunchKernelGGL(k_tail<1>, dim3(tiles), dim3(256), 0, s, in, H, W, w, out, oh, ow);
+    else return false;
     return true;
 }
 
