@@ -14,6 +14,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <map>
 #include <memory>
@@ -57,6 +58,7 @@ struct scunet_hip {
     std::map<std::string, std::pair<float*, size_t>> arena;
 
     bool prof = false;
+    bool unfused_msa = false;            // route every level through the 3-launch attention half
     std::string tag;                     // appended to profiler class names ("@L0".."@L3")
     std::vector<ProfRec> recs;
     std::vector<hipEvent_t> ev_pool;
@@ -247,6 +249,34 @@ bool block_scratch(scunet_hip* h, long P, int t, BlockScratch* s) {
     return true;
 }
 
+// The window-attention half as three launches (LN1+qkv GEMM, attention kernel,
+// proj GEMM with the residual): the path for t >= 128, where the token plane is small.
+bool msa_unfused(scunet_hip* h, const std::string& p, float* yt, int c, int t, int H, int Wd, int shift,
+                 const BlockScratch& s) {
+    const long P = long(H) * Wd;
+    const std::string tp = p + ".trans_block";
+    GemmArgs g;
+    g.A = yt; g.lda = c; g.ln_g = W(h, tp + ".ln1.weight"); g.ln_b = W(h, tp + ".ln1.bias");
+    g.W = W(h, tp + ".msa.embedding_layer.weight"); g.bias = W(h, tp + ".msa.embedding_layer.bias");
+    g.C = s.qkv; g.ldc = 3 * t; g.M = P; g.N = 3 * t; g.K = t;
+    if (!run_gemm(h, "qkv_ln", g, A_LN, E_STORE)) return false;
+    {
+        AttnArgs a;
+        a.qkv = s.qkv; a.ldq = 3 * t; a.out = s.o; a.ldo = t; a.tab = h->tab[p];
+        a.C = t; a.heads = t / h->wt.head_dim; a.nwh = H / 8; a.nww = Wd / 8; a.H = H; a.W = Wd;
+        a.shift = shift; a.pixel_mode = 1; a.scale = h->scale;
+        long nw = long(a.nwh) * a.nww;
+        Span sp(h, "attention", 16384.0 * t * nw, 4.0 * 64.0 * nw * 4 * t);
+        const char* why = nullptr;
+        if (!attention(a, h->stream, &why)) return fail(h, why);
+        if (!launched(h, "attention")) return false;
+    }
+    g = GemmArgs{};
+    g.A = s.o; g.lda = t; g.W = W(h, tp + ".msa.linear.weight"); g.bias = W(h, tp + ".msa.linear.bias");
+    g.C = yt; g.ldc = c; g.R = yt; g.ldr = c; g.M = P; g.N = t; g.K = t;
+    return run_gemm(h, "proj", g, A_ROWS, E_RESID);
+}
+
 // One ConvTransBlock in place on x [P][c] (cpu.rs:869-970; cuda.rs:1063-1146).
 bool block(scunet_hip* h, const std::string& p, float* x, int H, int Wd, int shift) {
     auto dims = h->wt.block_dims(p);
@@ -272,26 +302,20 @@ bool block(scunet_hip* h, const std::string& p, float* x, int H, int Wd, int shi
     if (!run_conv3(h, cv, false)) return false;
     // transformer half, tokens = pixels of y[:, t:2t].
     float* yt = s.y + t;
-    g = GemmArgs{};
-    g.A = yt; g.lda = c; g.ln_g = W(h, tp + ".ln1.weight"); g.ln_b = W(h, tp + ".ln1.bias");
-    g.W = W(h, tp + ".msa.embedding_layer.weight"); g.bias = W(h, tp + ".msa.embedding_layer.bias");
-    g.C = s.qkv; g.ldc = 3 * t; g.M = P; g.N = 3 * t; g.K = t;
-    if (!run_gemm(h, "qkv_ln", g, A_LN, E_STORE)) return false;
-    {
-        AttnArgs a;
-        a.qkv = s.qkv; a.ldq = 3 * t; a.out = s.o; a.ldo = t; a.tab = h->tab[p];
-        a.C = t; a.heads = t / h->wt.head_dim; a.nwh = H / 8; a.nww = Wd / 8; a.H = H; a.W = Wd;
-        a.shift = shift; a.pixel_mode = 1; a.scale = h->scale;
-        long nw = long(a.nwh) * a.nww;
-        Span sp(h, "attention", 16384.0 * t * nw, 4.0 * 64.0 * nw * 4 * t);
+    if (t <= 64 && !h->unfused_msa) {
+        MsaArgs m;
+        m.x = yt; m.ldx = c; m.ln_g = W(h, tp + ".ln1.weight"); m.ln_b = W(h, tp + ".ln1.bias");
+        m.wqkv = W(h, tp + ".msa.embedding_layer.weight"); m.bqkv = W(h, tp + ".msa.embedding_layer.bias");
+        m.wp = W(h, tp + ".msa.linear.weight"); m.bp = W(h, tp + ".msa.linear.bias"); m.tab = h->tab[p];
+        m.t = t; m.nwh = H / 8; m.nww = Wd / 8; m.H = H; m.W = Wd; m.shift = shift; m.scale = h->scale;
+        const double nw = double(m.nwh) * m.nww;
+        Span sp(h, "msa_fused", 64.0 * nw * (8.0 * t * t) + 16384.0 * t * nw, 4.0 * (2.0 * P * t + 4.0 * t * t));
         const char* why = nullptr;
-        if (!attention(a, h->stream, &why)) return fail(h, why);
-        if (!launched(h, "attention")) return false;
+        if (!msa_fused(m, h->stream, &why)) return fail(h, why);
+        if (!launched(h, "msa_fused")) return false;
+    } else if (!msa_unfused(h, p, yt, c, t, H, Wd, shift, s)) {
+        return false;
     }
-    g = GemmArgs{};
-    g.A = s.o; g.lda = t; g.W = W(h, tp + ".msa.linear.weight"); g.bias = W(h, tp + ".msa.linear.bias");
-    g.C = yt; g.ldc = c; g.R = yt; g.ldr = c; g.M = P; g.N = t; g.K = t;
-    if (!run_gemm(h, "proj", g, A_ROWS, E_RESID)) return false;
     {
         MlpArgs m;
         m.x = yt; m.ldx = c; m.ln_g = W(h, tp + ".ln2.weight"); m.ln_b = W(h, tp + ".ln2.bias");
@@ -507,6 +531,8 @@ int scunet_hip_create(const char* path, scunet_hip** out) {
         return 1;
     }
     h->scale = std::pow(float(h->wt.head_dim), -0.5f);
+    // A/B switch: run the window-attention half as three launches at every level.
+    h->unfused_msa = std::getenv("SCUNET_HIP_UNFUSED_MSA") != nullptr;
     if (!upload_weights(h.get())) {
         g_create_error = h->err;
         return 1;

@@ -95,6 +95,26 @@ struct AttnArgs {
 };
 // 8x8 windows, head_dim 32 only.
 bool attention(const AttnArgs& a, hipStream_t s, const char** why);
+
+// The whole window-attention half of a Swin block, fused per window (cpu.rs:791-799):
+// x += proj(attention(qkv(LN1(x)))) + proj bias, x being the [P][ldx] token plane with
+// t = T columns. q/k/v, the logits and the attention output never leave the CU.
+struct MsaArgs {
+    float* x = nullptr;
+    long ldx = 0;
+    const float* ln_g = nullptr;
+    const float* ln_b = nullptr;
+    const float* wqkv = nullptr;   // [3t][t]
+    const float* bqkv = nullptr;   // [3t]
+    const float* wp = nullptr;     // [t][t]
+    const float* bp = nullptr;     // [t]
+    const float* tab = nullptr;    // [heads][64][64] lane-ordered rel-pos bias
+    int t = 0;
+    int nwh = 0, nww = 0, H = 0, W = 0, shift = 0;
+    float scale = 0.f;
+};
+// t = 32 or 64 (the full-resolution and half-resolution stages); false otherwise.
+bool msa_fused(const MsaArgs& a, hipStream_t s, const char** why);
 // Host-side construction of the lane-ordered bias table from rp [heads][15][15].
 void build_bias_table(const float* rp, int heads, float* tab);
 

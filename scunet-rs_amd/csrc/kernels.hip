@@ -940,6 +940,209 @@ bool attention(const AttnArgs& a, hipStream_t s, const char** why) {
     return true;
 }
 
+// ---------------------------------------------------------------------------
+// Fused window attention half: one wave per 8x8 window, all heads.
+//   1. the window's 64 token rows are read through the shifted index map, LayerNormed in
+//      registers and parked in this wave's LDS slice;
+//   2. per head: Q^T = Wq Xn^T and K^T = Wk Xn^T (head dims as the MFMA rows) land with
+//      each lane holding 4 consecutive dims of one token - the operand layout of
+//      S^T = K Q^T - and V = Xn Wv^T (tokens as rows) lands in the operand layout of
+//      O^T = V^T P^T; softmax as in k_attention; O^T is then already the B operand of the
+//      projection out^T += Wp_h O^T, accumulated over heads in registers;
+//   3. x += out + bias, written back through the same index map (a permutation, so each
+//      window owns its 64 rows).
+// ---------------------------------------------------------------------------
+template <int T>
+__global__ __launch_bounds__(256) void k_msa(MsaArgs a, long nw) {
+    constexpr int HEADS = T / 32, KG = T / 16, OT = T / 16, LDX = T + 4;
+    __shared__ float xs[4 * 64 * LDX];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int li = lane & 15, lg = lane >> 4;
+    const long wi = long(blockIdx.x) * 4 + wave;
+    const bool valid = wi < nw;
+    const int wh = valid ? int(wi / a.nww) : 0, ww = valid ? int(wi - long(wh) * a.nww) : 0;
+    float* xw = xs + wave * 64 * LDX;
+    auto rowof = [&](int t) -> long {
+        int y = wh * 8 + (t >> 3) + a.shift;
+        int x = ww * 8 + (t & 7) + a.shift;
+        if (y >= a.H) y -= a.H;
+        if (x >= a.W) x -= a.W;
+        return long(y) * a.W + x;
+    };
+
+    // 1. LN1 of the window's tokens into LDS.
+    if (valid) {
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+            const long row = rowof(mt * 16 + li);
+            f4 v[KG];
+#pragma unroll
+            for (int kg = 0; kg < KG; ++kg) v[kg] = ld4(a.x + row * a.ldx + kg * 16 + lg * 4);
+            float sm = 0.f;
+#pragma unroll
+            for (int kg = 0; kg < KG; ++kg) sm += (v[kg].x + v[kg].y) + (v[kg].z + v[kg].w);
+            sm += __shfl_xor(sm, 16);
+            sm += __shfl_xor(sm, 32);
+            const float mu = sm / float(T);
+            float q = 0.f;
+#pragma unroll
+            for (int kg = 0; kg < KG; ++kg) {
+                f4 d = v[kg] - mu;
+                q += (d.x * d.x + d.y * d.y) + (d.z * d.z + d.w * d.w);
+            }
+            q += __shfl_xor(q, 16);
+            q += __shfl_xor(q, 32);
+            const float rs = 1.0f / sqrtf(q / float(T) + 1e-5f);
+#pragma unroll
+            for (int kg = 0; kg < KG; ++kg) {
+                f4 gg = ld4(a.ln_g + kg * 16 + lg * 4), bb = ld4(a.ln_b + kg * 16 + lg * 4);
+                st4(xw + (mt * 16 + li) * LDX + kg * 16 + lg * 4, (v[kg] - mu) * rs * gg + bb);
+            }
+        }
+    }
+    __syncthreads();
+    if (!valid) return;   // no barrier follows
+
+    const bool row_edge = a.shift > 0 && wh == a.nwh - 1;
+    const bool col_edge = a.shift > 0 && ww == a.nww - 1;
+    const float SENT = -3.4028234663852886e38f / 4.0f;
+    f4 acc[4][OT];
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+        for (int ot = 0; ot < OT; ++ot) acc[nt][ot] = f4{0.f, 0.f, 0.f, 0.f};
+
+#pragma unroll 1
+    for (int h = 0; h < HEADS; ++h) {
+        f4 qf[4][2], kf[4][2], vf[4][2];
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+            for (int d = 0; d < 2; ++d) qf[mt][d] = kf[mt][d] = vf[mt][d] = f4{0.f, 0.f, 0.f, 0.f};
+        const float* wq = a.wqkv + long(h * 32) * T;
+        const float* wk = a.wqkv + long(T + h * 32) * T;
+        const float* wv = a.wqkv + long(2 * T + h * 32) * T;
+#pragma unroll
+        for (int kg = 0; kg < KG; ++kg) {
+            f4 xb[4];
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt) xb[mt] = ld4(xw + (mt * 16 + li) * LDX + kg * 16 + lg * 4);
+#pragma unroll
+            for (int d = 0; d < 2; ++d) {
+                const f4 fq = ld4(wq + (d * 16 + li) * T + kg * 16 + lg * 4);
+                const f4 fk = ld4(wk + (d * 16 + li) * T + kg * 16 + lg * 4);
+                const f4 fv = ld4(wv + (d * 16 + li) * T + kg * 16 + lg * 4);
+#pragma unroll
+                for (int s = 0; s < 4; ++s)
+#pragma unroll
+                    for (int mt = 0; mt < 4; ++mt) {
+                        qf[mt][d] = mfma4(fq[s], xb[mt][s], qf[mt][d]);
+                        kf[mt][d] = mfma4(fk[s], xb[mt][s], kf[mt][d]);
+                        vf[mt][d] = mfma4(xb[mt][s], fv[s], vf[mt][d]);
+                    }
+            }
+        }
+        // Biases: qf/kf lanes hold dims 16d + 4lg .. +3 of token 16mt + li; vf lanes hold
+        // dim 16d + li of tokens 16mt + 4lg .. +3.
+#pragma unroll
+        for (int d = 0; d < 2; ++d) {
+            const f4 bq = ld4(a.bqkv + h * 32 + d * 16 + lg * 4);
+            const f4 bk = ld4(a.bqkv + T + h * 32 + d * 16 + lg * 4);
+            const float bv = a.bqkv[2 * T + h * 32 + d * 16 + li];
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt) {
+                qf[mt][d] += bq;
+                kf[mt][d] += bk;
+                vf[mt][d] += bv;
+            }
+        }
+        const float* tab = a.tab + (long(h) * 64 + lane) * 64;
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) {
+            f4 S[4];
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt) S[mt] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int G = 0; G < 2; ++G)
+#pragma unroll
+                for (int s = 0; s < 4; ++s)
+#pragma unroll
+                    for (int mt = 0; mt < 4; ++mt) S[mt] = mfma4(kf[mt][G][s], qf[nt][G][s], S[mt]);
+            const bool q_row_lo = nt < 2;
+            const bool q_col_lo = (li & 7) < 4;
+            const bool k_col_lo = (lg & 1) == 0;
+            float mx = -INFINITY;
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt) {
+                const f4 b = ld4(tab + nt * 16 + mt * 4);
+                const bool hit = (row_edge && (q_row_lo != (mt < 2))) || (col_edge && (q_col_lo != k_col_lo));
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    float v = S[mt][r] * a.scale + b[r];
+                    if (hit) v = SENT;
+                    S[mt][r] = v;
+                    mx = fmaxf(mx, v);
+                }
+            }
+            mx = fmaxf(mx, __shfl_xor(mx, 16));
+            mx = fmaxf(mx, __shfl_xor(mx, 32));
+            float sum = 0.0f;
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const float e = __expf(S[mt][r] - mx);
+                    S[mt][r] = e;
+                    sum += e;
+                }
+            sum += __shfl_xor(sum, 16);
+            sum += __shfl_xor(sum, 32);
+            const float inv = 1.0f / sum;
+            f4 O[2] = {f4{0.f, 0.f, 0.f, 0.f}, f4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+            for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const float p = S[kt][r] * inv;
+#pragma unroll
+                    for (int nd = 0; nd < 2; ++nd) O[nd] = mfma4(vf[kt][nd][r], p, O[nd]);
+                }
+            // out^T += Wp[:, head dims] O^T.
+#pragma unroll
+            for (int ot = 0; ot < OT; ++ot)
+#pragma unroll
+                for (int nd = 0; nd < 2; ++nd) {
+                    const f4 fw = ld4(a.wp + long(ot * 16 + li) * T + h * 32 + nd * 16 + lg * 4);
+#pragma unroll
+                    for (int s = 0; s < 4; ++s) acc[nt][ot] = mfma4(fw[s], O[nd][s], acc[nt][ot]);
+                }
+        }
+    }
+    // 3. Residual: lanes hold outputs 16ot + 4lg .. +3 of token 16nt + li.
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) {
+        const long row = rowof(nt * 16 + li);
+#pragma unroll
+        for (int ot = 0; ot < OT; ++ot) {
+            float* o = a.x + row * a.ldx + ot * 16 + lg * 4;
+            st4(o, ld4(o) + (acc[nt][ot] + ld4(a.bp + ot * 16 + lg * 4)));
+        }
+    }
+}
+
+bool msa_fused(const MsaArgs& a, hipStream_t s, const char** why) {
+    const long nw = long(a.nwh) * a.nww;
+    if (nw == 0) return true;
+    dim3 grid{unsigned((nw + 3) / 4), 1u, 1u}, block{256u, 1u, 1u};
+    if (a.t == 32) hipLaunchKernelGGL(k_msa<32>, grid, block, 0, s, a, nw);
+    else if (a.t == 64) hipLaunchKernelGGL(k_msa<64>, grid, block, 0, s, a, nw);
+    else {
+        *why = "msa_fused: t must be 32 or 64";
+        return false;
+    }
+    return true;
+}
+
 void build_bias_table(const float* rp, int heads, float* tab) {
     // tab[h][lane][nt][mt][r] = B_h[query 16nt + lane%16][key 16mt + 4(lane/16) + r],
     // B_h[p][q] = rp[h][(p/8 - q/8 + 7)][(p%8 - q%8 + 7)]   (cpu.rs:532-546).
