@@ -65,6 +65,46 @@ def cpu_baseline(weights_path, sample_hw):
             "seconds": round(dt, 3)}
 
 
+def attention_sweep(be, wpath, iters):
+    """the isolated window-attention core (the reference's kernel boundary,
+    qkv -> out, cuda.rs:767-808) at each level's 1920x1088 window grid, W and SW. x ~ N(0,1)
+    [nw*64][C]; qkv = x Wqkv^T + b with the level's seeded embedding weights; rel-pos
+    tables ~ N(0, 0.02) in upstream's [225][heads] storage, re-viewed to [heads][15][15]."""
+    import numpy as np
+    from scunet_hip.safetensors_io import read_safetensors
+    t, _ = read_safetensors(wpath)
+    out = []
+    for level in range(4):
+        c = 32 << level
+        heads = c // 32
+        nwh, nww = 136 >> level, 240 >> level
+        nw = nwh * nww
+        rng = np.random.default_rng(500 + level)
+        x = rng.standard_normal((nw * 64, c), dtype=np.float32)
+        name = ["m_down1.0", "m_down2.0", "m_down3.0", "m_body.0"][level] + ".trans_block.msa.embedding_layer"
+        qkv = np.ascontiguousarray(x @ np.asarray(t[name + ".weight"]).T + np.asarray(t[name + ".bias"]),
+                                   dtype=np.float32)
+        del x
+        raw = np.clip(rng.standard_normal((225, heads)) * 0.02, -0.04, 0.04)
+        rp = raw.reshape(15, 15, heads).transpose(0, 2, 1).transpose(1, 0, 2).astype(np.float32)
+        qp = be.malloc(qkv.nbytes)
+        op = be.malloc(qkv.nbytes // 3)
+        be.h2d(qp, qkv)
+        for shift in (0, 4):
+            ms = be.bench_attn(qp, rp, op, nwh, nww, c, heads, shift, iters)
+            flop = 16384.0 * c * nw
+            byts = 4.0 * 64 * nw * 4 * c
+            out.append({"level": level, "C": c, "heads": heads, "windows": nw, "shift": shift,
+                        "ms": round(ms, 5), "tflops": round(flop / (ms * 1e-3) / 1e12, 3),
+                        "gbs": round(byts / (ms * 1e-3) / 1e9, 1),
+                        "frac_hbm": round(byts / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)})
+            log(f"  attention C={c:3d} nw={nw:5d} shift={shift}: {ms * 1e3:8.1f} us, "
+                f"{out[-1]['tflops']:7.2f} TFLOP/s, {out[-1]['gbs']:7.1f} GB/s ({100 * out[-1]['frac_hbm']:.1f}% of HBM)")
+        be.free(qp)
+        be.free(op)
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -74,6 +114,7 @@ def main():
     ap.add_argument("--cpu-sample", type=int, nargs=2, default=(512, 512))
     ap.add_argument("--no-kernel-events", action="store_true",
                     help="time the steps without the per-launch event pairs")
+    ap.add_argument("--no-attn-sweep", action="store_true", help="skip the config-5 attention sweep")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         log("bench.py: this build runs one image on one GPU; multi-GPU runs are not part of it "
@@ -148,6 +189,11 @@ def main():
         agg = classes["attention"]
         attn_tflops = round(agg[2] / (agg[1] * 1e-3) / 1e12, 3)
 
+    sweep = None
+    if not args.no_attn_sweep:
+        log("bench: config-5 attention operator sweep")
+        sweep = attention_sweep(be, wpath, 20)
+
     cpu = None
     if not args.no_cpu_baseline:
         log(f"bench: CPU baseline (oracle) on {tuple(args.cpu_sample)} ...")
@@ -175,6 +221,8 @@ def main():
         "roofline": dominant,
         "attention_tflops": attn_tflops,
         "attention_roofline": attn,
+        "fused_window_attention_roofline": next((k for k in kernels if k["kernel"] == "msa_fused"), None),
+        "attention_sweep": sweep,
         "kernels": kernels,
         "cpu_baseline": cpu,
         "device_bytes": {"weights": fp[0], "scratch": fp[1]},

@@ -66,3 +66,10 @@ def max_abs(want, got):
     assert want.shape == got.shape
     assert np.isfinite(got).all()
     return float(np.abs(want - got).max())
+
+
+@pytest.fixture(scope="session")
+def weights_path_gray():
+    """The grayscale variant (in_nc = 1), BASELINE config 4's network."""
+    from scunet_hip import synth
+    return synth.weights_file(seed=5, in_nc=1)
