@@ -115,6 +115,9 @@ def main():
     ap.add_argument("--no-kernel-events", action="store_true",
                     help="time the steps without the per-launch event pairs")
     ap.add_argument("--no-attn-sweep", action="store_true", help="skip the config-5 attention sweep")
+    ap.add_argument("--profile-pass", action="store_true",
+                    help="for rocprofv3 counter runs: one forward plus one 256 MiB device copy (the "
+                         "calibration kernel), nothing else; prints no JSON line")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         log("bench.py: this build runs one image on one GPU; multi-GPU runs are not part of it "
@@ -135,6 +138,19 @@ def main():
     be.h2d(xp, x)
     log(f"bench: SCUNet-color {c}x{h}x{w} (padded {plan.hp}x{plan.wp}) on {be.name()}, "
         f"warmup {args.warmup}, steps {args.steps}")
+
+    if args.profile_pass:
+        nbytes = 256 << 20
+        a_, b_ = be.malloc(nbytes), be.malloc(nbytes)
+        be.copy(b_, a_, nbytes)
+        be.synchronize()
+        be.run_device(xp, c, h, w, yp)
+        be.synchronize()
+        be.free(a_)
+        be.free(b_)
+        log("bench: profile pass done (1 forward, 1 copy of 256 MiB)")
+        be.close()
+        return
 
     for _ in range(args.warmup):
         be.run_device(xp, c, h, w, yp)

@@ -95,6 +95,11 @@ int scunet_hip_free(scunet_hip* h, void* p);
 int scunet_hip_h2d(scunet_hip* h, void* dst, const void* src, size_t bytes);
 int scunet_hip_d2h(scunet_hip* h, void* dst, const void* src, size_t bytes);
 
+/* A plain streaming device-to-device copy kernel on the handle's stream (no counterpart
+ * in the reference): the known-size kernel that hardware traffic counters are
+ * calibrated against. bytes must be a multiple of 16 and both pointers 16-byte aligned. */
+int scunet_hip_copy(scunet_hip* h, void* dst, const void* src, size_t bytes);
+
 /* --- probes (src/cuda.rs:1153-1597), host buffers in the reference's layouts --- */
 
 /* Cuda::block_dump (cuda.rs:1153-1167): one ConvTransBlock `prefix` on x [c][hh][ww]. */

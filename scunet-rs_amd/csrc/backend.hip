@@ -699,6 +699,16 @@ int scunet_hip_d2h(scunet_hip* h, void* dst, const void* src, size_t bytes) {
     });
 }
 
+int scunet_hip_copy(scunet_hip* h, void* dst, const void* src, size_t bytes) {
+    return guard(h, [&] {
+        if (bytes % 16 || (reinterpret_cast<uintptr_t>(dst) | reinterpret_cast<uintptr_t>(src)) % 16)
+            return fail(h, "scunet_hip_copy: bytes and pointers must be 16-byte aligned");
+        Span sp(h, "copy", 0.0, 2.0 * double(bytes));
+        copy_f4(src, dst, long(bytes / 16), h->stream);
+        return launched(h, "copy");
+    });
+}
+
 // ---------------------------------------------------------------------------
 // Probes
 // ---------------------------------------------------------------------------

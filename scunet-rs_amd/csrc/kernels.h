@@ -128,6 +128,9 @@ bool head_conv(const float* x, int cin, int hh, int ww, int H, int W, const floa
 bool tail_conv(const float* in, int dim, int H, int W, const float* w, int cout, float* out,
                int oh, int ow, hipStream_t s);
 
+// A streaming copy of n float4 (the counter-calibration kernel).
+void copy_f4(const void* src, void* dst, long n, hipStream_t s);
+
 // Layout changes for the host boundary, probes and stage dumps.
 void nchw_to_nhwc(const float* src, float* dst, int c, long P, long ld, hipStream_t s);
 void nhwc_to_nchw(const float* src, float* dst, int c, long P, long ld, hipStream_t s);

@@ -11,6 +11,7 @@
 // as A and B agree on it.
 #include "kernels.h"
 
+#include <algorithm>
 #include <cmath>
 #include <cstdint>
 
@@ -40,7 +41,9 @@ DEVI long xcd_swizzle(long b, long nb) {
 // (cpu.rs:293-332), evaluated in fp32 (|erf error| < 1.5e-7 + fp32 rounding).
 DEVI float gelu_as(float v) {
     float x = v * 0.70710678118654752440f;
-    float t = 1.0f / (1.0f + 0.3275911f * fabsf(x));
+    // v_rcp_f32 (1 ulp) instead of an IEEE division: t enters a polynomial whose own
+    // approximation error is 1.5e-7, so a 1-ulp reciprocal changes nothing measurable.
+    float t = __builtin_amdgcn_rcpf(1.0f + 0.3275911f * fabsf(x));
     float y = 1.0f - (((((1.061405429f * t - 1.453152027f) * t) + 1.421413741f) * t - 0.284496736f) * t +
                       0.254829592f) * t * __expf(-x * x);
     float e = x >= 0.0f ? y : -y;
@@ -435,8 +438,7 @@ static void launch_gemm2_a(const GemmArgs& g, GemmA a, GemmE e, hipStream_t s) {
     }
 }
 
-// Tile choice: the widest N block (<= 128) that divides N; 256 rows per workgroup for
-// N <= 64, 128 above; 32-wide K slices.
+// Tile choice (32-wide K slices): see the comment in the body.
 static bool launch_gemm2(const GemmArgs& g, GemmA a, GemmE e, hipStream_t s) {
     if (a == A_LN) {
         switch (g.K) {
@@ -447,7 +449,10 @@ static bool launch_gemm2(const GemmArgs& g, GemmA a, GemmE e, hipStream_t s) {
         }
         return false;
     }
-    if (g.N % 128 == 0) launch_gemm2_a<2, 128, 32>(g, a, e, s);
+    // Measured on the 1080p forward: for N <= 128, 64-wide N blocks and 32-row waves (more
+    // waves per SIMD) beat wider tiles; above, 128-wide blocks.
+    if (g.N % 64 == 0 && g.N <= 128) launch_gemm2_a<2, 64, 32>(g, a, e, s);
+    else if (g.N % 128 == 0) launch_gemm2_a<2, 128, 32>(g, a, e, s);
     else if (g.N % 96 == 0) launch_gemm2_a<2, 96, 32>(g, a, e, s);
     else if (g.N % 64 == 0) launch_gemm2_a<4, 64, 32>(g, a, e, s);
     else if (g.N % 32 == 0) launch_gemm2_a<4, 32, 32>(g, a, e, s);
@@ -1333,6 +1338,15 @@ void nchw_to_nhwc(const float* src, float* dst, int c, long P, long ld, hipStrea
 void nhwc_to_nchw(const float* src, float* dst, int c, long P, long ld, hipStream_t s) {
     dim3 grid(unsigned((P + 31) / 32), unsigned((c + 31) / 32));
     hipLaunchKernelGGL(k_nhwc_to_nchw, grid, dim3(256), 0, s, src, dst, c, P, ld);
+}
+
+__global__ void k_copy_f4(const f4* __restrict__ src, f4* __restrict__ dst, long n) {
+    for (long i = long(blockIdx.x) * 256 + threadIdx.x; i < n; i += long(gridDim.x) * 256) dst[i] = src[i];
+}
+
+void copy_f4(const void* src, void* dst, long n, hipStream_t s) {
+    const unsigned blocks = unsigned(std::min<long>((n + 255) / 256, 256L * 64));
+    hipLaunchKernelGGL(k_copy_f4, dim3(blocks), dim3(256), 0, s, static_cast<const f4*>(src), static_cast<f4*>(dst), n);
 }
 
 // The window map of the attention kernel (win_row, pixel mode), as a copy.

@@ -27,6 +27,7 @@ EXPORTS = [
     "scunet_hip_forward_dump", "scunet_hip_run", "scunet_hip_run_device", "scunet_hip_footprint",
     "scunet_hip_release_scratch", "scunet_hip_synchronize", "scunet_hip_stream", "scunet_hip_profile",
     "scunet_hip_profile_report", "scunet_hip_malloc", "scunet_hip_free", "scunet_hip_h2d", "scunet_hip_d2h",
+    "scunet_hip_copy",
     "scunet_hip_block_probe", "scunet_hip_op_probe", "scunet_hip_linear_probe",
     "scunet_hip_layer_norm_probe", "scunet_hip_attention_kernel_probe", "scunet_hip_gather_probe",
     "scunet_hip_window_round_trip", "scunet_hip_attention_probe", "scunet_hip_bench_attn",
@@ -81,6 +82,7 @@ def load_library(path=None):
     L.scunet_hip_free.argtypes = [_vp, _vp]
     L.scunet_hip_h2d.argtypes = [_vp, _vp, _vp, _sz]
     L.scunet_hip_d2h.argtypes = [_vp, _vp, _vp, _sz]
+    L.scunet_hip_copy.argtypes = [_vp, _vp, _vp, _sz]
     L.scunet_hip_block_probe.argtypes = [_vp, ctypes.c_char_p, _sz, _sz, _sz, _f, _f]
     L.scunet_hip_op_probe.argtypes = [_vp, ctypes.c_char_p, ctypes.c_char_p, _f, _sz, _sz, _sz, _sz, _f]
     L.scunet_hip_linear_probe.argtypes = [_vp, ctypes.c_char_p, _f, _sz, _sz, _sz, _f]
@@ -267,6 +269,10 @@ class Hip:
     def d2h(self, arr, ptr):
         self._check(self._lib.scunet_hip_d2h(self._h, arr.ctypes.data_as(_vp), _vp(ptr), arr.nbytes))
         return arr
+
+    def copy(self, dst, src, nbytes):
+        """A plain device copy kernel (the traffic-counter calibration kernel)."""
+        self._check(self._lib.scunet_hip_copy(self._h, _vp(dst), _vp(src), nbytes))
 
     def forward_device(self, xptr, c, hp, wp, yptr):
         self._check(self._lib.scunet_hip_forward_device(self._h, _vp(xptr), c, hp, wp, _vp(yptr)))
