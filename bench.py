@@ -48,6 +48,17 @@ def roofline_of(name, launches, ms, flop, byts):
             "algorithmic_bytes_per_launch": byts / launches}
 
 
+def measured_traffic():
+    """HBM bytes per launch per kernel class, from the calibrated FETCH_SIZE/WRITE_SIZE
+    counter passes summarised in profiles/counters_1080p.md (machine-readable copy:
+    profiles/traffic_1080p.json). None when the file is absent."""
+    p = os.path.join(REPO, "profiles", "traffic_1080p.json")
+    if not os.path.exists(p):
+        return {}
+    with open(p) as f:
+        return json.load(f).get("classes", {})
+
+
 def cpu_baseline(weights_path, sample_hw):
     """The oracle (C++ restatement of the reference's src/cpu.rs) on a bounded sample."""
     sys.path.insert(0, os.path.join(REPO, "oracle"))
@@ -198,6 +209,12 @@ def main():
         for lvl, v in sorted(k["levels"].items()):
             log(f"  {'':>14}   {lvl}: {v['avg_launch_ms'] * 1e3:9.1f} us avg, {v['ms_per_step']:7.3f} ms/step, "
                 f"{v['achieved']:9.2f} {v['unit']} ({100 * v['frac']:.1f}%)")
+    traffic = measured_traffic()
+    for k in kernels:
+        t = traffic.get(k["kernel"])
+        if t and t["launches"] * args.steps == k["launches"]:
+            k["traffic"] = round(t["traffic_bytes_per_launch"])
+            k["traffic_source"] = "profiles/counters_1080p.md"
     dominant = kernels[0] if kernels else None
     attn = next((k for k in kernels if k["kernel"] == "attention"), None)
     attn_tflops = None
