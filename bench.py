@@ -209,6 +209,19 @@ def main():
         for lvl, v in sorted(k["levels"].items()):
             log(f"  {'':>14}   {lvl}: {v['avg_launch_ms'] * 1e3:9.1f} us avg, {v['ms_per_step']:7.3f} ms/step, "
                 f"{v['achieved']:9.2f} {v['unit']} ({100 * v['frac']:.1f}%)")
+    # The conv-block 3x3 convolutions run as Winograd F(2x2,3x3) unless SCUNET_HIP_DIRECT3X3
+    # is set: `achieved` counts the direct convolution's 18*cin*cout FLOP per pixel (the
+    # algorithm of the reference), the MFMA units execute 8*cin*cout per pixel (16 products
+    # per 2x2 output tile); the transforms run on the vector ALUs and are not counted.
+    if not os.environ.get("SCUNET_HIP_DIRECT3X3"):
+        for k in kernels:
+            if k["kernel"] == "conv3x3":
+                ex = k["achieved"] * 8.0 / 18.0
+                k["algorithm"] = "winograd F(2x2,3x3); achieved/frac count direct-convolution FLOP"
+                k["executed_mfma_tflops"] = round(ex, 3)
+                k["executed_frac"] = round(ex / PEAK_FP32_TFLOPS, 4)
+                log(f"  conv3x3 (Winograd): {ex:.2f} TFLOP/s executed on MFMA "
+                    f"({100 * ex / PEAK_FP32_TFLOPS:.1f}% of peak)")
     traffic = measured_traffic()
     for k in kernels:
         t = traffic.get(k["kernel"])

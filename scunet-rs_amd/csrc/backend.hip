@@ -59,6 +59,7 @@ struct scunet_hip {
 
     bool prof = false;
     bool unfused_msa = false;            // route every level through the 3-launch attention half
+    bool direct3x3 = false;              // the direct implicit-GEMM 3x3 instead of Winograd
     std::string tag;                     // appended to profiler class names ("@L0".."@L3")
     std::vector<ProfRec> recs;
     std::vector<hipEvent_t> ev_pool;
@@ -175,6 +176,9 @@ bool upload_weights(scunet_hip* h) {
             for (size_t o = 0; o < co; ++o)
                 for (size_t i = 0; i < ci; ++i)
                     for (size_t tap = 0; tap < 9; ++tap) v[(tap * co + o) * ci + i] = t.data[(o * ci + i) * 9 + tap];
+            std::vector<float> u(16 * co * ci);
+            winograd_filter(t.data, int(co), int(ci), u.data());
+            host.push_back({"@wino:" + n, std::move(u)});
         } else if (is_down(n)) {
             size_t co = t.shape[0], ci = t.shape[1];
             for (size_t o = 0; o < co; ++o)
@@ -205,7 +209,7 @@ bool upload_weights(scunet_hip* h) {
         if (!ck(h, hipMemcpy(at, e.second.data(), e.second.size() * 4, hipMemcpyHostToDevice), "weight upload"))
             return false;
         if (e.first.rfind("@tab:", 0) == 0) h->tab[e.first.substr(5)] = reinterpret_cast<float*>(at);
-        else h->w[e.first] = reinterpret_cast<float*>(at);
+        else h->w[e.first] = reinterpret_cast<float*>(at);   // "@wino:<name>" are Winograd filters
         at += (e.second.size() * 4 + 255) / 256 * 256;
     }
     return true;
@@ -224,12 +228,22 @@ bool run_gemm(scunet_hip* h, const char* cls, const GemmArgs& g, GemmA a, GemmE 
     return launched(h, cls);
 }
 
-bool run_conv3(scunet_hip* h, const Conv3Args& c, bool relu) {
+// A conv_block 3x3 convolution `name` (".weight" appended): Winograd F(2x2,3x3) unless the
+// handle was created with the direct kernel selected. FLOP are counted as the direct
+// form's (18 cin cout per pixel), so both paths report comparable rates.
+bool run_conv3(scunet_hip* h, const std::string& name, Conv3Args c, bool relu) {
     long P = long(c.H) * c.W;
     Span sp(h, "conv3x3", 18.0 * double(P) * c.cin * c.cout,
             4.0 * (double(P) * (c.cin + c.cout * (relu ? 1 : 2)) + 9.0 * c.cin * c.cout));
     const char* why = nullptr;
-    if (!conv3x3(c, relu, h->stream, &why)) return fail(h, why);
+    const float* u = W(h, "@wino:" + name + ".weight");
+    if (!h->direct3x3 && u && c.cin % 16 == 0 && c.cout % 16 == 0 && c.H % 2 == 0 && c.W % 2 == 0) {
+        c.w = u;
+        if (!conv3x3_winograd(c, relu, h->stream, &why)) return fail(h, why);
+    } else {
+        c.w = W(h, name + ".weight");
+        if (!conv3x3(c, relu, h->stream, &why)) return fail(h, why);
+    }
     return launched(h, "conv3x3");
 }
 
@@ -295,11 +309,11 @@ bool block(scunet_hip* h, const std::string& p, float* x, int H, int Wd, int shi
     if (!run_gemm(h, "conv1x1", g, A_ROWS, E_STORE)) return false;
     // conv half: s1 = relu(conv3x3(y[:, :t])); y[:, :t] += conv3x3(s1).
     Conv3Args cv;
-    cv.in = s.y; cv.ldi = c; cv.w = W(h, p + ".conv_block.0.weight"); cv.out = s.s1; cv.ldo = t;
+    cv.in = s.y; cv.ldi = c; cv.out = s.s1; cv.ldo = t;
     cv.H = H; cv.W = Wd; cv.cin = t; cv.cout = t;
-    if (!run_conv3(h, cv, true)) return false;
-    cv.in = s.s1; cv.ldi = t; cv.w = W(h, p + ".conv_block.2.weight"); cv.out = s.y; cv.ldo = c;
-    if (!run_conv3(h, cv, false)) return false;
+    if (!run_conv3(h, p + ".conv_block.0", cv, true)) return false;
+    cv.in = s.s1; cv.ldi = t; cv.out = s.y; cv.ldo = c;
+    if (!run_conv3(h, p + ".conv_block.2", cv, false)) return false;
     // transformer half, tokens = pixels of y[:, t:2t].
     float* yt = s.y + t;
     if (t <= 64 && !h->unfused_msa) {
@@ -533,6 +547,8 @@ int scunet_hip_create(const char* path, scunet_hip** out) {
     h->scale = std::pow(float(h->wt.head_dim), -0.5f);
     // A/B switch: run the window-attention half as three launches at every level.
     h->unfused_msa = std::getenv("SCUNET_HIP_UNFUSED_MSA") != nullptr;
+    // A/B switch: the direct implicit-GEMM 3x3 kernel instead of Winograd F(2x2,3x3).
+    h->direct3x3 = std::getenv("SCUNET_HIP_DIRECT3X3") != nullptr;
     if (!upload_weights(h.get())) {
         g_create_error = h->err;
         return 1;
@@ -767,10 +783,10 @@ int scunet_hip_op_probe(scunet_hip* h, const char* op, const char* name, const f
             nchw_to_nhwc(dx, xt, int(c_in), P, long(c_in), h->stream);
             if (o == "conv3x3") {
                 Conv3Args cv;
-                cv.in = xt; cv.ldi = long(c_in); cv.w = wp; cv.out = yt; cv.ldo = long(c_out);
+                cv.in = xt; cv.ldi = long(c_in); cv.out = yt; cv.ldo = long(c_out);
                 cv.H = int(hh); cv.W = int(ww); cv.cin = int(c_in); cv.cout = int(c_out);
                 if (!ck(h, hipMemsetAsync(yt, 0, c_out * size_t(P) * 4, h->stream), "memset")) return false;
-                if (!run_conv3(h, cv, false)) return false;
+                if (!run_conv3(h, n, cv, false)) return false;
             } else {
                 GemmArgs g;
                 g.A = xt; g.lda = long(c_in); g.W = wp; g.C = yt; g.ldc = long(c_out);

@@ -79,6 +79,11 @@ struct Conv3Args {
 };
 // relu=true: out = relu(conv); relu=false: out += conv (the conv half's residual).
 bool conv3x3(const Conv3Args& a, bool relu, hipStream_t s, const char** why);
+// The same convolution by Winograd F(2x2, 3x3); a.w is the transformed filter
+// U = G g G^T laid out [16][cout][cin] (see winograd_filter). cin, cout multiples of 16.
+bool conv3x3_winograd(const Conv3Args& a, bool relu, hipStream_t s, const char** why);
+// Host-side filter transform: g [cout][cin][3][3] -> U [16][cout][cin] (in double).
+void winograd_filter(const float* g, int cout, int cin, float* u);
 
 struct AttnArgs {
     const float* qkv = nullptr;    // rows of [q | k | v], each C wide

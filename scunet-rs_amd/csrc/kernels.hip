@@ -813,6 +813,171 @@ bool conv3x3(const Conv3Args& a, bool relu, hipStream_t s, const char** why) {
 }
 
 // ---------------------------------------------------------------------------
+// 3x3 convolution by Winograd F(2x2, 3x3) on the matrix cores (Lavin & Gray 2016,
+// "Fast Algorithms for Convolutional Neural Networks"): each 2x2 output tile is
+// Y = A^T [ (G g G^T) .* (B^T d B) ] A summed over input channels, with d the tile's 4x4
+// input patch and
+//     B^T = [1 0 -1 0; 0 1 1 0; 0 -1 1 0; 0 1 0 -1]
+//     G   = [1 0 0; 1/2 1/2 1/2; 1/2 -1/2 1/2; 0 0 1]      (applied on the host)
+//     A^T = [1 1 1 0; 0 1 -1 -1]
+// so the channel sum becomes 16 independent products M[xi] = U[xi] V[xi] (xi = 4i + j over
+// the transformed 4x4 positions), 2.25x fewer multiplies than the direct form.
+// Workgroup: 16x16 output pixels (8x8 tiles) x 16 output channels, 4 waves; wave w owns
+// tile rows 2w, 2w+1 (16 tiles, the MFMA N dimension: lane li = tile). Per 16-channel
+// slice: the 18x18 halo and U[16][16 co][16 ci] go through LDS; each lane reads its tile's
+// 4x4 patch for 4 consecutive channels (lane group lg), transforms it in registers into
+// exactly the B operand it supplies, and M^T[xi] = U[xi] V[xi]^T accumulates in 16 x 4
+// registers. Every lane then holds all 16 M[xi] for its tile and 4 consecutive channels,
+// so the output transform and the float4 store are lane-local.
+// ---------------------------------------------------------------------------
+template <bool RELU>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_wino(Conv3Args a) {
+    constexpr int BK = 16, LDC = BK + 4, HW = 18;
+    constexpr int HV = (HW * HW * 4 + 255) / 256;   // halo float4 per thread
+    constexpr int UV = 16 * 16 * 4 / 256;           // U float4 per thread
+    __shared__ float Hs[HW * HW * LDC];
+    __shared__ float Us[16 * 16 * LDC];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int li = lane & 15, lg = lane >> 4;
+    const int tx = (a.W + 15) >> 4, nb = a.cout / 16;
+    const long tile = xcd_swizzle(blockIdx.x, gridDim.x);
+    const int co0 = int(tile % nb) * 16;
+    const long sp = tile / nb;
+    const int y0 = int(sp / tx) * 16, x0 = int(sp % tx) * 16;
+    const int tr = 2 * wave + (li >> 3), tc = li & 7;
+
+    f4 rh[HV], ru[UV];
+    auto load = [&](int ci0) {
+#pragma unroll
+        for (int i = 0; i < HV; ++i) {
+            const int f = tid + i * 256;
+            f4 v = {0.f, 0.f, 0.f, 0.f};
+            if (f < HW * HW * 4) {
+                const int px = f >> 2, c4 = f & 3;
+                const int gy = y0 - 1 + px / HW, gx = x0 - 1 + px % HW;
+                if (gy >= 0 && gy < a.H && gx >= 0 && gx < a.W)
+                    v = ld4(a.in + (long(gy) * a.W + gx) * a.ldi + ci0 + c4 * 4);
+            }
+            rh[i] = v;
+        }
+#pragma unroll
+        for (int i = 0; i < UV; ++i) {
+            const int f = tid + i * 256;
+            const int xi = f >> 6, rem = f & 63, co = rem >> 2, c4 = rem & 3;
+            ru[i] = ld4(a.w + (long(xi) * a.cout + co0 + co) * a.cin + ci0 + c4 * 4);
+        }
+    };
+    auto stash = [&]() {
+#pragma unroll
+        for (int i = 0; i < HV; ++i) {
+            const int f = tid + i * 256;
+            if (f < HW * HW * 4) st4(&Hs[(f >> 2) * LDC + (f & 3) * 4], rh[i]);
+        }
+#pragma unroll
+        for (int i = 0; i < UV; ++i) {
+            const int f = tid + i * 256;
+            st4(&Us[(f >> 2) * LDC + (f & 3) * 4], ru[i]);
+        }
+    };
+
+    f4 acc[16];
+#pragma unroll
+    for (int xi = 0; xi < 16; ++xi) acc[xi] = f4{0.f, 0.f, 0.f, 0.f};
+
+    load(0);
+    stash();
+    __syncthreads();
+    for (int ci0 = 0; ci0 < a.cin; ci0 += BK) {
+        const bool more = ci0 + BK < a.cin;
+        if (more) load(ci0 + BK);
+        // T = B^T d column by column (each needs one column of the patch), then row i of
+        // V = T B feeds the products for xi = 4i .. 4i+3 (channels 4lg .. 4lg+3).
+        f4 t[4][4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float* col = &Hs[((2 * tr) * HW + 2 * tc + j) * LDC + lg * 4];
+            const f4 d0 = ld4(col), d1 = ld4(col + HW * LDC), d2 = ld4(col + 2 * HW * LDC),
+                     d3 = ld4(col + 3 * HW * LDC);
+            t[0][j] = d0 - d2;
+            t[1][j] = d1 + d2;
+            t[2][j] = d2 - d1;
+            t[3][j] = d1 - d3;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const f4 v[4] = {t[i][0] - t[i][2], t[i][1] + t[i][2], t[i][2] - t[i][1], t[i][1] - t[i][3]};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const f4 u = ld4(&Us[((i * 4 + j) * 16 + li) * LDC + lg * 4]);
+#pragma unroll
+                for (int s = 0; s < 4; ++s) acc[i * 4 + j] = mfma4(u[s], v[j][s], acc[i * 4 + j]);
+            }
+        }
+        __syncthreads();
+        if (more) {
+            stash();
+            __syncthreads();
+        }
+    }
+    // Output transform: lane holds M[xi] for its tile, channels co0 + 4lg .. +3.
+    f4 s0[4], s1[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        s0[j] = acc[j] + acc[4 + j] + acc[8 + j];
+        s1[j] = acc[4 + j] - acc[8 + j] - acc[12 + j];
+    }
+    f4 yv[2][2];
+    yv[0][0] = s0[0] + s0[1] + s0[2];
+    yv[0][1] = s0[1] - s0[2] - s0[3];
+    yv[1][0] = s1[0] + s1[1] + s1[2];
+    yv[1][1] = s1[1] - s1[2] - s1[3];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int y = y0 + 2 * tr + i, x = x0 + 2 * tc + j;
+            if (y >= a.H || x >= a.W) continue;
+            float* o = a.out + (long(y) * a.W + x) * a.ldo + co0 + lg * 4;
+            f4 v = yv[i][j];
+            if constexpr (RELU) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) v[r] = fmaxf(v[r], 0.0f);
+                st4(o, v);
+            } else {
+                st4(o, ld4(o) + v);
+            }
+        }
+}
+
+bool conv3x3_winograd(const Conv3Args& a, bool relu, hipStream_t s, const char** why) {
+    if (a.cin % 16 != 0 || a.cout % 16 != 0 || (a.H & 1) || (a.W & 1)) {
+        *why = "conv3x3_winograd: cin and cout must be multiples of 16 and the plane even";
+        return false;
+    }
+    const long tiles = long((a.W + 15) / 16) * ((a.H + 15) / 16) * (a.cout / 16);
+    dim3 grid{unsigned(tiles), 1u, 1u}, block{256u, 1u, 1u};
+    if (relu) hipLaunchKernelGGL(k_wino<true>, grid, block, 0, s, a);
+    else hipLaunchKernelGGL(k_wino<false>, grid, block, 0, s, a);
+    return true;
+}
+
+void winograd_filter(const float* g, int cout, int cin, float* u) {
+    static const double G[4][3] = {{1, 0, 0}, {0.5, 0.5, 0.5}, {0.5, -0.5, 0.5}, {0, 0, 1}};
+    for (int o = 0; o < cout; ++o)
+        for (int c = 0; c < cin; ++c) {
+            const float* k = g + (long(o) * cin + c) * 9;
+            double t[4][3];
+            for (int i = 0; i < 4; ++i)
+                for (int j = 0; j < 3; ++j) t[i][j] = G[i][0] * k[j] + G[i][1] * k[3 + j] + G[i][2] * k[6 + j];
+            for (int i = 0; i < 4; ++i)
+                for (int j = 0; j < 4; ++j)
+                    u[(long(i * 4 + j) * cout + o) * cin + c] =
+                        float(t[i][0] * G[j][0] + t[i][1] * G[j][1] + t[i][2] * G[j][2]);
+        }
+}
+
+// ---------------------------------------------------------------------------
 // Window attention, 8x8 windows (64 tokens), head_dim 32. One wave per (window, head).
 //   S^T = K Q^T on MFMA (keys are the M rows, queries the N columns), so after the
 //   product each lane holds, for ONE query, 16 of its 64 key logits; the other 48

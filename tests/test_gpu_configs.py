@@ -137,3 +137,33 @@ def test_1080p_properties(be):
     y = be.forward(np.ascontiguousarray(pad_replicate(x, plan.hp, plan.wp), dtype=np.float32), plan)
     assert np.array_equal(a, y[:, :h, :w])
     assert 0.0 < float(np.abs(a).mean()) < 10.0
+
+
+def test_direct_and_winograd_3x3_agree(weights_path, owt):
+    """The conv half's 3x3 convolutions by Winograd F(2x2,3x3) (the default) and by the
+    direct implicit GEMM: both against the oracle's cpu.rs conv3x3, op by op and in a block."""
+    from scunet_hip import Hip, synth
+    os.environ["SCUNET_HIP_DIRECT3X3"] = "1"
+    try:
+        direct = Hip(weights_path)
+    finally:
+        del os.environ["SCUNET_HIP_DIRECT3X3"]
+    wino = Hip(weights_path)
+    try:
+        for name, c, h, w in (("m_down1.0.conv_block.0", 32, 40, 24), ("m_down2.1.conv_block.2", 64, 16, 24),
+                              ("m_down3.2.conv_block.0", 128, 24, 16), ("m_body.0.conv_block.2", 256, 16, 16)):
+            x = synth.seq(c * h * w, 0.37).reshape(c, h, w)
+            want = O.conv3x3(x, owt.t[name + ".weight"])
+            a = wino.op_probe("conv3x3", name, x, c, c, h, w)
+            b = direct.op_probe("conv3x3", name, x, c, c, h, w)
+            close(f"winograd {name}", want, a, 1e-5)
+            close(f"direct {name}", want, b, 1e-5)
+        for prefix, shift in (("m_down1.1", 4), ("m_body.2", 0)):
+            c = sum(owt.block_dims(prefix))
+            x = synth.seq(c * 24 * 32, 0.61).reshape(c, 24, 32)
+            want = O.conv_trans_block(owt, prefix, x, shift)
+            assert max_abs(want, wino.block_dump(prefix, 24, 32, shift, x)) <= STAGE_TOL
+            assert max_abs(want, direct.block_dump(prefix, 24, 32, shift, x)) <= STAGE_TOL
+    finally:
+        wino.close()
+        direct.close()
