@@ -60,6 +60,7 @@ struct scunet_hip {
     bool prof = false;
     bool unfused_msa = false;            // route every level through the 3-launch attention half
     bool direct3x3 = false;              // the direct implicit-GEMM 3x3 instead of Winograd
+    bool gemm1x1 = false;                // the tiled GEMM for every 1x1 (no resident weights, no chaining)
     std::string tag;                     // appended to profiler class names ("@L0".."@L3")
     std::vector<ProfRec> recs;
     std::vector<hipEvent_t> ev_pool;
@@ -291,8 +292,25 @@ bool msa_unfused(scunet_hip* h, const std::string& p, float* yt, int c, int t, i
     return run_gemm(h, "proj", g, A_ROWS, E_RESID);
 }
 
+// A block's 1x1 convolution through the resident-weight kernel; FLOP and bytes as for
+// the GEMM form (the chained form counts both products and both outputs).
+bool run_pconv(scunet_hip* h, const PconvArgs& a, PconvMode mode) {
+    const double P = double(a.M), c = a.c;
+    const double flop = 2.0 * P * c * c * (mode == PC_CHAIN ? 2 : 1);
+    const double bytes = 4.0 * (P * c * (mode == PC_STORE ? 2 : mode == PC_RESID ? 3 : 4) +
+                                c * c * (mode == PC_CHAIN ? 2 : 1));
+    Span sp(h, mode == PC_CHAIN ? "conv1x1_chain" : "conv1x1", flop, bytes);
+    const char* why = nullptr;
+    if (!pconv(a, mode, h->stream, &why)) return fail(h, why);
+    return launched(h, "conv1x1");
+}
+
 // One ConvTransBlock in place on x [P][c] (cpu.rs:869-970; cuda.rs:1063-1146).
-bool block(scunet_hip* h, const std::string& p, float* x, int H, int Wd, int shift) {
+// y_ready: the previous block's chained epilogue already wrote this block's conv1_1
+// output into the block scratch. next: the following block of the same stage, whose
+// conv1_1 is then chained onto this block's conv1_2 (empty for the last block).
+bool block(scunet_hip* h, const std::string& p, float* x, int H, int Wd, int shift, bool y_ready = false,
+           const std::string& next = std::string()) {
     auto dims = h->wt.block_dims(p);
     const int t = dims.second, conv = dims.first, c = conv + t;
     if (conv != t) return fail(h, p + ": conv and trans halves of different widths are not supported");
@@ -301,12 +319,19 @@ bool block(scunet_hip* h, const std::string& p, float* x, int H, int Wd, int shi
     if (!block_scratch(h, P, t, &s)) return false;
     const std::string tp = p + ".trans_block";
 
+    const bool resident = pconv_supported(c) && !h->gemm1x1;
+    if (y_ready && !resident) return fail(h, p + ": chained conv1_1 needs the resident-weight kernel");
     GemmArgs g;
     // conv1_1: y = x W^T + b.
-    g = GemmArgs{};
-    g.A = x; g.lda = c; g.W = W(h, p + ".conv1_1.weight"); g.bias = W(h, p + ".conv1_1.bias");
-    g.C = s.y; g.ldc = c; g.M = P; g.N = c; g.K = c;
-    if (!run_gemm(h, "conv1x1", g, A_ROWS, E_STORE)) return false;
+    if (resident && !y_ready) {
+        PconvArgs a;
+        a.A = x; a.W = W(h, p + ".conv1_1.weight"); a.b = W(h, p + ".conv1_1.bias"); a.C = s.y; a.M = P; a.c = c;
+        if (!run_pconv(h, a, PC_STORE)) return false;
+    } else if (!resident) {
+        g.A = x; g.lda = c; g.W = W(h, p + ".conv1_1.weight"); g.bias = W(h, p + ".conv1_1.bias");
+        g.C = s.y; g.ldc = c; g.M = P; g.N = c; g.K = c;
+        if (!run_gemm(h, "conv1x1", g, A_ROWS, E_STORE)) return false;
+    }
     // conv half: s1 = relu(conv3x3(y[:, :t])); y[:, :t] += conv3x3(s1).
     Conv3Args cv;
     cv.in = s.y; cv.ldi = c; cv.out = s.s1; cv.ldo = t;
@@ -340,11 +365,35 @@ bool block(scunet_hip* h, const std::string& p, float* x, int H, int Wd, int shi
         if (!mlp(m, h->stream, &why)) return fail(h, why);
         if (!launched(h, "mlp")) return false;
     }
-    // conv1_2 on the concatenation, residual over the block: x += y W^T + b.
+    // conv1_2 on the concatenation, residual over the block: x += y W^T + b; chained with
+    // the next block's conv1_1 (y = x W1^T + b1) when there is one.
+    if (resident) {
+        PconvArgs a;
+        a.A = s.y; a.W = W(h, p + ".conv1_2.weight"); a.b = W(h, p + ".conv1_2.bias");
+        a.R = x; a.C = x; a.M = P; a.c = c;
+        if (next.empty()) return run_pconv(h, a, PC_RESID);
+        a.W1 = W(h, next + ".conv1_1.weight"); a.b1 = W(h, next + ".conv1_1.bias"); a.C2 = s.y;
+        return run_pconv(h, a, PC_CHAIN);
+    }
     g = GemmArgs{};
     g.A = s.y; g.lda = c; g.W = W(h, p + ".conv1_2.weight"); g.bias = W(h, p + ".conv1_2.bias");
     g.C = x; g.ldc = c; g.R = x; g.ldr = c; g.M = P; g.N = c; g.K = c;
     return run_gemm(h, "conv1x1", g, A_ROWS, E_RESID);
+}
+
+// The `count` blocks `prefix` first .. first+count-1 of one stage, in place on x; block i
+// uses the shifted windows when i is odd (cpu.rs:1216-1222, 1298-1302). With the resident-weight 1x1
+// kernel, each block's conv1_2 is chained with the next block's conv1_1.
+bool stage_blocks(scunet_hip* h, const std::string& prefix, int first, int count, float* x, int H, int Wd) {
+    const int win = h->wt.window;
+    const int c = h->wt.block_dims(prefix + std::to_string(first)).first * 2;
+    const bool chain = pconv_supported(c) && !h->gemm1x1;
+    for (int i = 0; i < count; ++i) {
+        const std::string next = chain && i + 1 < count ? prefix + std::to_string(first + i + 1) : std::string();
+        if (!block(h, prefix + std::to_string(first + i), x, H, Wd, (i & 1) ? win / 2 : 0, chain && i > 0, next))
+            return false;
+    }
+    return true;
 }
 
 bool dump_plane(scunet_hip* h, scunet_stage_hook hook, void* user, const char* name, const float* plane,
@@ -399,9 +448,7 @@ bool walk(scunet_hip* h, const float* x, int hh, int ww, int H, int Wd, float* y
         const int count = wt.config[k];
         const int c = dim << k;
         h->tag = "@L" + std::to_string(k);
-        for (int i = 0; i < count; ++i)
-            if (!block(h, "m_" + name + "." + std::to_string(i), cur[k], Hs[k], Ws[k], (i & 1) ? wt.window / 2 : 0))
-                return false;
+        if (!stage_blocks(h, "m_" + name + ".", 0, count, cur[k], Hs[k], Ws[k])) return false;
         if (!dump_plane(h, hook, user, ("m_" + name + "_blocks").c_str(), cur[k], c, P[k])) return false;
         GemmArgs g;
         g.A = cur[k]; g.lda = c; g.W = W(h, "m_" + name + "." + std::to_string(count) + ".weight");
@@ -411,9 +458,7 @@ bool walk(scunet_hip* h, const float* x, int hh, int ww, int H, int Wd, float* y
         if (!dump_plane(h, hook, user, ("m_" + name).c_str(), skip[k + 1], 2 * c, P[k + 1])) return false;
     }
     h->tag = "@L3";
-    for (int i = 0; i < wt.config[3]; ++i)
-        if (!block(h, "m_body." + std::to_string(i), cur[3], Hs[3], Ws[3], (i & 1) ? wt.window / 2 : 0))
-            return false;
+    if (!stage_blocks(h, "m_body.", 0, wt.config[3], cur[3], Hs[3], Ws[3])) return false;
     if (!dump_plane(h, hook, user, "m_body", cur[3], dim << 3, P[3])) return false;
     for (int k = 0; k < 3; ++k) {
         const std::string name = STAGE[4 + k];
@@ -426,10 +471,7 @@ bool walk(scunet_hip* h, const float* x, int hh, int ww, int H, int Wd, float* y
         g.C = cur[lvl]; g.M = P[lvl + 1]; g.N = 4 * co; g.K = ci; g.in_w = Ws[lvl + 1]; g.cout = co;
         if (!run_gemm(h, "up2x2", g, A_ADD2, E_D2S)) return false;
         if (!dump_plane(h, hook, user, ("m_" + name + "_up").c_str(), cur[lvl], co, P[lvl])) return false;
-        for (int i = 0; i < wt.config[4 + k]; ++i)
-            if (!block(h, "m_" + name + "." + std::to_string(i + 1), cur[lvl], Hs[lvl], Ws[lvl],
-                       (i & 1) ? wt.window / 2 : 0))
-                return false;
+        if (!stage_blocks(h, "m_" + name + ".", 1, wt.config[4 + k], cur[lvl], Hs[lvl], Ws[lvl])) return false;
         if (!dump_plane(h, hook, user, ("m_" + name).c_str(), cur[lvl], co, P[lvl])) return false;
     }
     h->tag.clear();
@@ -549,6 +591,7 @@ int scunet_hip_create(const char* path, scunet_hip** out) {
     h->unfused_msa = std::getenv("SCUNET_HIP_UNFUSED_MSA") != nullptr;
     // A/B switch: the direct implicit-GEMM 3x3 kernel instead of Winograd F(2x2,3x3).
     h->direct3x3 = std::getenv("SCUNET_HIP_DIRECT3X3") != nullptr;
+    h->gemm1x1 = std::getenv("SCUNET_HIP_GEMM1X1") != nullptr;
     if (!upload_weights(h.get())) {
         g_create_error = h->err;
         return 1;
@@ -791,7 +834,11 @@ int scunet_hip_op_probe(scunet_hip* h, const char* op, const char* name, const f
                 GemmArgs g;
                 g.A = xt; g.lda = long(c_in); g.W = wp; g.C = yt; g.ldc = long(c_out);
                 g.N = int(c_out);
-                if (o == "conv1x1") {
+                if (o == "conv1x1" && c_in == c_out && pconv_supported(int(c_in)) && bp && !h->gemm1x1) {
+                    PconvArgs a;
+                    a.A = xt; a.W = wp; a.b = bp; a.C = yt; a.M = P; a.c = int(c_in);
+                    if (!run_pconv(h, a, PC_STORE)) return false;
+                } else if (o == "conv1x1") {
                     g.bias = bp; g.M = P; g.K = int(c_in);
                     if (!run_gemm(h, "conv1x1", g, A_ROWS, E_STORE)) return false;
                 } else if (o == "conv2x2s2") {

@@ -52,6 +52,30 @@ struct GemmArgs {
 // Returns false (and a reason) if no tile configuration fits the shape.
 bool gemm(const GemmArgs& g, GemmA a, GemmE e, hipStream_t s, const char** why);
 
+// A block's 1x1 convolutions over c channels (in = out = c, row stride c) with the whole
+// weight matrix resident in LDS, for c in {64, 128}:
+//   PC_STORE: C = A W^T + b                     (conv1_1, cpu.rs:869-872)
+//   PC_RESID: C = R + A W^T + b                 (conv1_2 + the block residual, cpu.rs:960-968)
+//   PC_CHAIN: C = R + A W^T + b, then C2 = C W1^T + b1: one block's conv1_2 and residual
+//             followed by the next block's conv1_1, without the block output leaving the CU.
+// In place is allowed (C == R, C2 == A): every row is read and written by one wave only.
+enum PconvMode { PC_STORE = 0, PC_RESID = 1, PC_CHAIN = 2 };
+struct PconvArgs {
+    const float* A = nullptr;
+    const float* W = nullptr;      // [c][c]
+    const float* b = nullptr;      // [c]
+    const float* R = nullptr;
+    float* C = nullptr;
+    const float* W1 = nullptr;     // PC_CHAIN: [c][c]
+    const float* b1 = nullptr;
+    float* C2 = nullptr;
+    long M = 0;
+    int c = 0;
+};
+// False (and a reason) for channel counts without a resident-weight configuration.
+bool pconv_supported(int c);
+bool pconv(const PconvArgs& a, PconvMode mode, hipStream_t s, const char** why);
+
 // The transformer half's MLP with its pre-norm and residual, fused (cpu.rs:800-860):
 // x[m] += W2 gelu(W0 LN(x[m]) + b0) + b2 for each row m of a [M][ldx] plane with t = T
 // columns. The 4t-wide hidden layer never leaves the CU.

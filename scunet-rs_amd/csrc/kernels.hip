@@ -24,6 +24,11 @@ typedef float f4 __attribute__((ext_vector_type(4)));
 DEVI f4 mfma4(float a, float b, f4 c) { return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0); }
 
 DEVI f4 ld4(const float* p) { return *reinterpret_cast<const f4*>(p); }
+// LDS row pitches: a wave's 16-byte LDS reads are conflict-free when, within each 32-lane
+// half, the 16-byte slot indices are distinct mod 32. The MFMA operand reads here have
+// lane li (0..15) on a row and lane group lg (0..1 per half) on 4 consecutive floats of
+// it, so a row pitch of P floats is conflict-free when P = 8 (mod 16) (P/4 twice an odd
+// number). Pitches below are the row width + 8 for that reason.
 DEVI void st4(float* p, f4 v) { *reinterpret_cast<f4*>(p) = v; }
 
 // Workgroups are dispatched round-robin over the 8 XCDs (workgroup b runs on XCD b % 8),
@@ -238,7 +243,7 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
 // ---------------------------------------------------------------------------
 template <int MT, int BN, int KC, int AM, int EP, int KLN>
 __global__ __launch_bounds__(256) void k_gemm2(GemmArgs g) {
-    constexpr int NT = BN / 16, KG = KC / 16, LDB = KC + 4;
+    constexpr int NT = BN / 16, KG = KC / 16, LDB = KC + 8;
     constexpr int BV = BN * KC / 4 / 256;
     static_assert(BN * KC / 4 % 256 == 0, "weight slice must split evenly over 256 threads");
     constexpr bool LN = AM == A_LN;
@@ -508,6 +513,160 @@ bool gemm(const GemmArgs& g, GemmA a, GemmE e, hipStream_t s, const char** why) 
 }
 
 // ---------------------------------------------------------------------------
+// Persistent 1x1 convolution with LDS-resident weights. A workgroup loads the [c][c]
+// weight matrix (two of them when chaining) into LDS once; then each wave on its own
+// walks 16*MT-row pixel groups with a grid stride: the next group's rows are loaded
+// while the current group is multiplied, so the HBM stream never waits on a workgroup
+// start-up or a barrier. The product is transposed as in k_gemm2 (weights as the MFMA
+// M rows), which leaves each lane holding 4 consecutive output channels of one pixel:
+// a float4 store, and, when chaining, exactly the pixel operand of the next product.
+// ---------------------------------------------------------------------------
+template <int C, int MT, int NW, int MODE>
+__global__ __launch_bounds__(NW * 64) void k_pconv(PconvArgs a) {
+    constexpr int NT = C / 16, KG = C / 16, LDW = C + 8;
+    constexpr int NMAT = MODE == PC_CHAIN ? 2 : 1;
+    __shared__ float Ws[NMAT * C * LDW];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int li = lane & 15, lg = lane >> 4;
+
+    for (int f = tid; f < NMAT * C * C / 4; f += NW * 64) {
+        const int m = f / (C * C / 4), r = (f / (C / 4)) % C, c4 = f % (C / 4);
+        const float* src = m ? a.W1 : a.W;
+        st4(&Ws[m * C * LDW + r * LDW + c4 * 4], ld4(src + long(r) * C + c4 * 4));
+    }
+    __syncthreads();
+
+    const long groups = (a.M + 16 * MT - 1) / (16 * MT);
+    const long stride = long(gridDim.x) * NW;
+    long gi = long(blockIdx.x) * NW + wave;
+
+    auto load = [&](long g, f4 (&dst)[MT][KG]) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+            const long row = g * 16 * MT + mt * 16 + li;
+#pragma unroll
+            for (int kg = 0; kg < KG; ++kg)
+                dst[mt][kg] = row < a.M ? ld4(a.A + row * C + kg * 16 + lg * 4) : f4{0.f, 0.f, 0.f, 0.f};
+        }
+    };
+    auto product = [&](const float* Wm, const f4 (&x)[MT][KG], f4 (&acc)[MT][NT]) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kg = 0; kg < KG; ++kg) {
+            f4 w[NT];
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) w[nt] = ld4(Wm + (nt * 16 + li) * LDW + kg * 16 + lg * 4);
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                    for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = mfma4(w[nt][s], x[mt][kg][s], acc[mt][nt]);
+        }
+    };
+
+    // One group: its rows are in `cur`; the group one stride ahead is loaded into `nxt`
+    // before the product, so that load overlaps this group's MFMAs and stores.
+    auto body = [&](long g, const f4 (&cur)[MT][KG], f4 (&nxt)[MT][KG]) {
+        f4 r[MT][NT];
+        if constexpr (MODE != PC_STORE) {
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+                const long row = g * 16 * MT + mt * 16 + li;
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt)
+                    r[mt][nt] = row < a.M ? ld4(a.R + row * C + nt * 16 + lg * 4) : f4{0.f, 0.f, 0.f, 0.f};
+            }
+        }
+        if (g + stride < groups) load(g + stride, nxt);
+        // The weights are loop-invariant; an opaque zero offset keeps the compiler from
+        // hoisting every LDS weight read out of the loop into registers.
+        int wz = 0;
+        asm volatile("" : "+v"(wz));
+        const float* Wg = Ws + wz;
+        f4 acc[MT][NT];
+        product(Wg, cur, acc);
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+            const f4 bv = ld4(a.b + nt * 16 + lg * 4);
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+                acc[mt][nt] = acc[mt][nt] + bv;
+                if constexpr (MODE != PC_STORE) acc[mt][nt] = r[mt][nt] + acc[mt][nt];
+                const long row = g * 16 * MT + mt * 16 + li;
+                if (row < a.M) st4(a.C + row * C + nt * 16 + lg * 4, acc[mt][nt]);
+            }
+        }
+        if constexpr (MODE == PC_CHAIN) {
+            f4 acc2[MT][NT];
+            product(Wg + C * LDW, acc, acc2);
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+                const f4 bv = ld4(a.b1 + nt * 16 + lg * 4);
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) {
+                    const long row = g * 16 * MT + mt * 16 + li;
+                    if (row < a.M) st4(a.C2 + row * C + nt * 16 + lg * 4, acc2[mt][nt] + bv);
+                }
+            }
+        }
+    };
+
+    f4 xa[MT][KG], xb[MT][KG];
+    if (gi < groups) load(gi, xa);
+    while (gi < groups) {
+        body(gi, xa, xb);
+        gi += stride;
+        if (gi >= groups) break;
+        body(gi, xb, xa);
+        gi += stride;
+    }
+}
+
+template <int C, int MT, int NW, int MODE>
+static bool launch_pconv(const PconvArgs& a, hipStream_t s) {
+    static int per_cu = -1, cus = 0;
+    if (per_cu < 0) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess) return false;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return false;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_pconv<C, MT, NW, MODE>, NW * 64, 0) !=
+            hipSuccess)
+            return false;
+        if (per_cu < 1) per_cu = 1;
+    }
+    const long groups = (a.M + 16 * MT - 1) / (16 * MT);
+    const long waves = std::min<long>(groups, long(cus) * per_cu * NW);
+    dim3 grid{unsigned((waves + NW - 1) / NW), 1u, 1u}, block{unsigned(NW * 64), 1u, 1u};
+    hipLaunchKernelGGL((k_pconv<C, MT, NW, MODE>), grid, block, 0, s, a);
+    return true;
+}
+
+bool pconv_supported(int c) { return c == 64 || c == 128; }
+
+bool pconv(const PconvArgs& a, PconvMode mode, hipStream_t s, const char** why) {
+    if (a.M <= 0) return true;
+    bool ok = false;
+    if (a.c == 64) {
+        if (mode == PC_STORE) ok = launch_pconv<64, 2, 4, PC_STORE>(a, s);
+        else if (mode == PC_RESID) ok = launch_pconv<64, 2, 4, PC_RESID>(a, s);
+        else ok = launch_pconv<64, 2, 4, PC_CHAIN>(a, s);
+    } else if (a.c == 128) {
+        if (mode == PC_STORE) ok = launch_pconv<128, 1, 4, PC_STORE>(a, s);
+        else if (mode == PC_RESID) ok = launch_pconv<128, 1, 4, PC_RESID>(a, s);
+        else ok = launch_pconv<128, 1, 8, PC_CHAIN>(a, s);
+    } else {
+        *why = "pconv: only 64 or 128 channels have a resident-weight configuration";
+        return false;
+    }
+    if (!ok) *why = "pconv: device query failed";
+    return ok;
+}
+
+// ---------------------------------------------------------------------------
 // Fused MLP: x += W2 gelu(W0 LN(x) + b0) + b2, t = T channels, hidden 4T.
 // Each wave owns 16*MT rows; LN runs on the rows in registers (the 4 lanes 16 apart hold
 // one row between them). The hidden layer is produced HC units at a time and TRANSPOSED
@@ -518,7 +677,7 @@ bool gemm(const GemmArgs& g, GemmA a, GemmE e, hipStream_t s, const char** why) 
 template <int T, int MT, int HC>
 __global__ __launch_bounds__(256) void k_mlp(MlpArgs a) {
     constexpr int KG = T / 16, NT = T / 16, HT = HC / 16, NCH = 4 * T / HC;
-    constexpr int L0 = T + 4, L2 = HC + 4;
+    constexpr int L0 = T + 8, L2 = HC + 8;
     constexpr int BUF = HC * L0 + T * L2;
     constexpr int W0V = HC * T / 4;               // float4 in a W0 slice
     constexpr int PV = (2 * W0V) / 256;           // float4 per thread per slice (W0 then W2)
@@ -822,40 +981,59 @@ bool conv3x3(const Conv3Args& a, bool relu, hipStream_t s, const char** why) {
 //     A^T = [1 1 1 0; 0 1 -1 -1]
 // so the channel sum becomes 16 independent products M[xi] = U[xi] V[xi] (xi = 4i + j over
 // the transformed 4x4 positions), 2.25x fewer multiplies than the direct form.
-// Workgroup: 16x16 output pixels (8x8 tiles) x 16 output channels, 4 waves; wave w owns
+// Unit of work: 16x16 output pixels (8x8 tiles) x 16 output channels, 4 waves; wave w owns
 // tile rows 2w, 2w+1 (16 tiles, the MFMA N dimension: lane li = tile). Per 16-channel
 // slice: the 18x18 halo and U[16][16 co][16 ci] go through LDS; each lane reads its tile's
 // 4x4 patch for 4 consecutive channels (lane group lg), transforms it in registers into
 // exactly the B operand it supplies, and M^T[xi] = U[xi] V[xi]^T accumulates in 16 x 4
 // registers. Every lane then holds all 16 M[xi] for its tile and 4 consecutive channels,
 // so the output transform and the float4 store are lane-local.
+// The grid is persistent (as many workgroups as fit on the chip at once); a workgroup
+// walks units with a grid stride, and the next (unit, slice) step's global loads are
+// issued before the current step's products, across unit boundaries too, so a unit's
+// first slice and its epilogue overlap the neighbouring steps. Units are numbered so that
+// the cout blocks of one spatial tile run on the same XCD (they read the same halo).
 // ---------------------------------------------------------------------------
+struct WinoUnit {
+    int y0, x0, co0;
+};
+DEVI WinoUnit wino_unit(long u, int tx, int nb, long tiles) {
+    // u = 8 j + xcd; within an XCD, consecutive j walk the cout blocks of one tile.
+    const long xcd = u & 7, j = u >> 3;
+    const long sp = (j / nb) * 8 + xcd;
+    WinoUnit w;
+    w.co0 = int(j % nb) * 16;
+    w.y0 = sp < tiles ? int(sp / tx) * 16 : -1;
+    w.x0 = int(sp % tx) * 16;
+    return w;
+}
+
 template <bool RELU>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_wino(Conv3Args a) {
-    constexpr int BK = 16, LDC = BK + 4, HW = 18;
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_wino(Conv3Args a, long tiles,
+                                                                                         long units) {
+    // Halo pixel (py, px) at Hs[(py * HP + px) * LDC]: 5 slots per pixel and 24-pixel rows
+    // make the patch reads (lanes 2 pixels apart along a row, two tile rows 2 pixel rows
+    // apart) hit 32 distinct slots mod 32 per half-wave; U rows are 24 floats apart.
+    constexpr int BK = 16, LDC = BK + 4, HW = 18, HP = 24, LDU = BK + 8;
     constexpr int HV = (HW * HW * 4 + 255) / 256;   // halo float4 per thread
     constexpr int UV = 16 * 16 * 4 / 256;           // U float4 per thread
-    __shared__ float Hs[HW * HW * LDC];
-    __shared__ float Us[16 * 16 * LDC];
+    __shared__ float Hs[HW * HP * LDC];
+    __shared__ float Us[16 * 16 * LDU];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int li = lane & 15, lg = lane >> 4;
-    const int tx = (a.W + 15) >> 4, nb = a.cout / 16;
-    const long tile = xcd_swizzle(blockIdx.x, gridDim.x);
-    const int co0 = int(tile % nb) * 16;
-    const long sp = tile / nb;
-    const int y0 = int(sp / tx) * 16, x0 = int(sp % tx) * 16;
+    const int tx = (a.W + 15) >> 4, nb = a.cout / 16, nch = a.cin / BK;
     const int tr = 2 * wave + (li >> 3), tc = li & 7;
 
     f4 rh[HV], ru[UV];
-    auto load = [&](int ci0) {
+    auto load = [&](const WinoUnit& w, int ci0) {
 #pragma unroll
         for (int i = 0; i < HV; ++i) {
             const int f = tid + i * 256;
             f4 v = {0.f, 0.f, 0.f, 0.f};
-            if (f < HW * HW * 4) {
+            if (f < HW * HW * 4 && w.y0 >= 0) {
                 const int px = f >> 2, c4 = f & 3;
-                const int gy = y0 - 1 + px / HW, gx = x0 - 1 + px % HW;
+                const int gy = w.y0 - 1 + px / HW, gx = w.x0 - 1 + px % HW;
                 if (gy >= 0 && gy < a.H && gx >= 0 && gx < a.W)
                     v = ld4(a.in + (long(gy) * a.W + gx) * a.ldi + ci0 + c4 * 4);
             }
@@ -865,89 +1043,99 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         for (int i = 0; i < UV; ++i) {
             const int f = tid + i * 256;
             const int xi = f >> 6, rem = f & 63, co = rem >> 2, c4 = rem & 3;
-            ru[i] = ld4(a.w + (long(xi) * a.cout + co0 + co) * a.cin + ci0 + c4 * 4);
+            ru[i] = ld4(a.w + (long(xi) * a.cout + w.co0 + co) * a.cin + ci0 + c4 * 4);
         }
     };
     auto stash = [&]() {
 #pragma unroll
         for (int i = 0; i < HV; ++i) {
             const int f = tid + i * 256;
-            if (f < HW * HW * 4) st4(&Hs[(f >> 2) * LDC + (f & 3) * 4], rh[i]);
+            if (f < HW * HW * 4) {
+                const int px = f >> 2;
+                st4(&Hs[((px / HW) * HP + px % HW) * LDC + (f & 3) * 4], rh[i]);
+            }
         }
 #pragma unroll
         for (int i = 0; i < UV; ++i) {
             const int f = tid + i * 256;
-            st4(&Us[(f >> 2) * LDC + (f & 3) * 4], ru[i]);
+            st4(&Us[(f >> 2) * LDU + (f & 3) * 4], ru[i]);
         }
     };
 
-    f4 acc[16];
+    long u = blockIdx.x;
+    if (u >= units) return;
+    WinoUnit cur = wino_unit(u, tx, nb, tiles);
+    load(cur, 0);
+    for (;;) {
+        f4 acc[16];
 #pragma unroll
-    for (int xi = 0; xi < 16; ++xi) acc[xi] = f4{0.f, 0.f, 0.f, 0.f};
-
-    load(0);
-    stash();
-    __syncthreads();
-    for (int ci0 = 0; ci0 < a.cin; ci0 += BK) {
-        const bool more = ci0 + BK < a.cin;
-        if (more) load(ci0 + BK);
-        // T = B^T d column by column (each needs one column of the patch), then row i of
-        // V = T B feeds the products for xi = 4i .. 4i+3 (channels 4lg .. 4lg+3).
-        f4 t[4][4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const float* col = &Hs[((2 * tr) * HW + 2 * tc + j) * LDC + lg * 4];
-            const f4 d0 = ld4(col), d1 = ld4(col + HW * LDC), d2 = ld4(col + 2 * HW * LDC),
-                     d3 = ld4(col + 3 * HW * LDC);
-            t[0][j] = d0 - d2;
-            t[1][j] = d1 + d2;
-            t[2][j] = d2 - d1;
-            t[3][j] = d1 - d3;
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const f4 v[4] = {t[i][0] - t[i][2], t[i][1] + t[i][2], t[i][2] - t[i][1], t[i][1] - t[i][3]};
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const f4 u = ld4(&Us[((i * 4 + j) * 16 + li) * LDC + lg * 4]);
-#pragma unroll
-                for (int s = 0; s < 4; ++s) acc[i * 4 + j] = mfma4(u[s], v[j][s], acc[i * 4 + j]);
-            }
-        }
-        __syncthreads();
-        if (more) {
+        for (int xi = 0; xi < 16; ++xi) acc[xi] = f4{0.f, 0.f, 0.f, 0.f};
+        const long un = u + gridDim.x;
+        const WinoUnit nxt = wino_unit(un, tx, nb, tiles);
+        for (int c = 0; c < nch; ++c) {
+            __syncthreads();
             stash();
             __syncthreads();
-        }
-    }
-    // Output transform: lane holds M[xi] for its tile, channels co0 + 4lg .. +3.
-    f4 s0[4], s1[4];
+            if (c + 1 < nch) load(cur, (c + 1) * BK);
+            else if (un < units) load(nxt, 0);
+            // T = B^T d column by column (each needs one column of the patch), then row i
+            // of V = T B feeds the products for xi = 4i .. 4i+3 (channels 4lg .. 4lg+3).
+            f4 t[4][4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        s0[j] = acc[j] + acc[4 + j] + acc[8 + j];
-        s1[j] = acc[4 + j] - acc[8 + j] - acc[12 + j];
-    }
-    f4 yv[2][2];
-    yv[0][0] = s0[0] + s0[1] + s0[2];
-    yv[0][1] = s0[1] - s0[2] - s0[3];
-    yv[1][0] = s1[0] + s1[1] + s1[2];
-    yv[1][1] = s1[1] - s1[2] - s1[3];
+            for (int j = 0; j < 4; ++j) {
+                const float* col = &Hs[((2 * tr) * HP + 2 * tc + j) * LDC + lg * 4];
+                const f4 d0 = ld4(col), d1 = ld4(col + HP * LDC), d2 = ld4(col + 2 * HP * LDC),
+                         d3 = ld4(col + 3 * HP * LDC);
+                t[0][j] = d0 - d2;
+                t[1][j] = d1 + d2;
+                t[2][j] = d2 - d1;
+                t[3][j] = d1 - d3;
+            }
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+            for (int i = 0; i < 4; ++i) {
+                const f4 v[4] = {t[i][0] - t[i][2], t[i][1] + t[i][2], t[i][2] - t[i][1], t[i][1] - t[i][3]};
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int y = y0 + 2 * tr + i, x = x0 + 2 * tc + j;
-            if (y >= a.H || x >= a.W) continue;
-            float* o = a.out + (long(y) * a.W + x) * a.ldo + co0 + lg * 4;
-            f4 v = yv[i][j];
-            if constexpr (RELU) {
+                for (int j = 0; j < 4; ++j) {
+                    const f4 uu = ld4(&Us[((i * 4 + j) * 16 + li) * LDU + lg * 4]);
 #pragma unroll
-                for (int r = 0; r < 4; ++r) v[r] = fmaxf(v[r], 0.0f);
-                st4(o, v);
-            } else {
-                st4(o, ld4(o) + v);
+                    for (int s4 = 0; s4 < 4; ++s4) acc[i * 4 + j] = mfma4(uu[s4], v[j][s4], acc[i * 4 + j]);
+                }
             }
         }
+        // Output transform: lane holds M[xi] for its tile, channels co0 + 4lg .. +3.
+        if (cur.y0 >= 0) {
+            f4 s0[4], s1[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                s0[j] = acc[j] + acc[4 + j] + acc[8 + j];
+                s1[j] = acc[4 + j] - acc[8 + j] - acc[12 + j];
+            }
+            f4 yv[2][2];
+            yv[0][0] = s0[0] + s0[1] + s0[2];
+            yv[0][1] = s0[1] - s0[2] - s0[3];
+            yv[1][0] = s1[0] + s1[1] + s1[2];
+            yv[1][1] = s1[1] - s1[2] - s1[3];
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const int y = cur.y0 + 2 * tr + i, x = cur.x0 + 2 * tc + j;
+                    if (y >= a.H || x >= a.W) continue;
+                    float* o = a.out + (long(y) * a.W + x) * a.ldo + cur.co0 + lg * 4;
+                    f4 v = yv[i][j];
+                    if constexpr (RELU) {
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) v[r] = fmaxf(v[r], 0.0f);
+                        st4(o, v);
+                    } else {
+                        st4(o, ld4(o) + v);
+                    }
+                }
+        }
+        if (un >= units) break;
+        u = un;
+        cur = nxt;
+    }
 }
 
 bool conv3x3_winograd(const Conv3Args& a, bool relu, hipStream_t s, const char** why) {
@@ -955,10 +1143,28 @@ bool conv3x3_winograd(const Conv3Args& a, bool relu, hipStream_t s, const char**
         *why = "conv3x3_winograd: cin and cout must be multiples of 16 and the plane even";
         return false;
     }
-    const long tiles = long((a.W + 15) / 16) * ((a.H + 15) / 16) * (a.cout / 16);
-    dim3 grid{unsigned(tiles), 1u, 1u}, block{256u, 1u, 1u};
-    if (relu) hipLaunchKernelGGL(k_wino<true>, grid, block, 0, s, a);
-    else hipLaunchKernelGGL(k_wino<false>, grid, block, 0, s, a);
+    static int per_cu[2] = {-1, -1}, cus = 0;
+    int& pc = per_cu[relu ? 1 : 0];
+    if (pc < 0) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&pc, relu ? k_wino<true> : k_wino<false>, 256, 0) !=
+                hipSuccess) {
+            *why = "conv3x3_winograd: device query failed";
+            return false;
+        }
+        if (pc < 1) pc = 1;
+    }
+    const long tiles = long((a.W + 15) / 16) * ((a.H + 15) / 16);
+    const int nb = a.cout / 16;
+    // Units are numbered 8 j + xcd with j < ceil(tiles / 8) * nb; numbers whose tile is
+    // past the end (the last partial group of 8) carry y0 = -1 and do no loads or stores.
+    const long units = ((tiles + 7) / 8) * 8 * nb;
+    const long grid = std::min<long>(units, long(cus) * pc);
+    dim3 g{unsigned(grid), 1u, 1u}, block{256u, 1u, 1u};
+    if (relu) hipLaunchKernelGGL(k_wino<true>, g, block, 0, s, a, tiles, units);
+    else hipLaunchKernelGGL(k_wino<false>, g, block, 0, s, a, tiles, units);
     return true;
 }
 

@@ -167,3 +167,45 @@ def test_direct_and_winograd_3x3_agree(weights_path, owt):
     finally:
         wino.close()
         direct.close()
+
+
+def test_resident_chained_1x1_and_tiled_gemm_agree(weights_path, owt):
+    """The 1x1 convolutions at 64 and 128 channels through the resident-weight kernel
+    (the default: each block's conv1_2 + residual chained with the next block's conv1_1)
+    and through the tiled GEMM (SCUNET_HIP_GEMM1X1): every stage of cpu.rs:1175-1321's
+    walker against the oracle, one block each, and the bare conv1_1 on pixel counts that
+    end in a partial 16- or 32-row group (the window grid makes every block's pixel count
+    a multiple of 64, so only the probe reaches those rows)."""
+    from scunet_hip import Hip, synth
+    os.environ["SCUNET_HIP_GEMM1X1"] = "1"
+    try:
+        tiled = Hip(weights_path)
+    finally:
+        del os.environ["SCUNET_HIP_GEMM1X1"]
+    chained = Hip(weights_path)
+    try:
+        for (h, w, seed) in ((64, 64, 31), (64, 192, 32)):
+            x = synth.noisy_image(seed, 3, h, w, 15)
+            _, want = O.forward_dump(owt, x)
+            for be in (chained, tiled):
+                got = {}
+                y = be.forward_dump(x, lambda n, v: got.__setitem__(n, v))
+                assert list(got) == list(want)
+                for name in want:
+                    d = max_abs(want[name], got[name])
+                    assert d <= STAGE_TOL, f"{be is chained} {h}x{w} {name}: {d:.3e}"
+        for prefix, shift in (("m_down1.0", 0), ("m_up2.2", 4)):
+            c = sum(owt.block_dims(prefix))
+            x = synth.seq(c * 24 * 40, 0.43).reshape(c, 24, 40)
+            want = O.conv_trans_block(owt, prefix, x, shift)
+            assert max_abs(want, chained.block_dump(prefix, 24, 40, shift, x)) <= STAGE_TOL
+            assert max_abs(want, tiled.block_dump(prefix, 24, 40, shift, x)) <= STAGE_TOL
+        for name, c, h, w in (("m_down1.2.conv1_1", 64, 7, 9), ("m_down1.3.conv1_1", 64, 21, 13),
+                              ("m_down2.0.conv1_1", 128, 5, 3), ("m_up2.1.conv1_1", 128, 17, 11)):
+            x = synth.seq(c * h * w, 0.29).reshape(c, h, w)
+            want = O.conv1x1(x, owt.t[name + ".weight"].reshape(c, c), owt.t[name + ".bias"])
+            close(f"resident {name} {h}x{w}", want, chained.op_probe("conv1x1", name, x, c, c, h, w), 1e-5)
+            close(f"tiled {name} {h}x{w}", want, tiled.op_probe("conv1x1", name, x, c, c, h, w), 1e-5)
+    finally:
+        chained.close()
+        tiled.close()
