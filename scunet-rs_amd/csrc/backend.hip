@@ -61,6 +61,7 @@ struct scunet_hip {
     bool unfused_msa = false;            // route every level through the 3-launch attention half
     bool direct3x3 = false;              // the direct implicit-GEMM 3x3 instead of Winograd
     bool gemm1x1 = false;                // the tiled GEMM for every 1x1 (no resident weights, no chaining)
+    bool separate_mlp = false;           // the MLP as its own kernel also at t = 32
     std::string tag;                     // appended to profiler class names ("@L0".."@L3")
     std::vector<ProfRec> recs;
     std::vector<hipEvent_t> ev_pool;
@@ -341,26 +342,36 @@ bool block(scunet_hip* h, const std::string& p, float* x, int H, int Wd, int shi
     if (!run_conv3(h, p + ".conv_block.2", cv, false)) return false;
     // transformer half, tokens = pixels of y[:, t:2t].
     float* yt = s.y + t;
+    const double mlp_flop = 16.0 * double(P) * t * t;
+    // At t = 32 the MLP runs inside the window kernel, on the window's tokens.
+    const bool mlp_in_msa = t == 32 && !h->unfused_msa && !h->separate_mlp;
     if (t <= 64 && !h->unfused_msa) {
         MsaArgs m;
         m.x = yt; m.ldx = c; m.ln_g = W(h, tp + ".ln1.weight"); m.ln_b = W(h, tp + ".ln1.bias");
         m.wqkv = W(h, tp + ".msa.embedding_layer.weight"); m.bqkv = W(h, tp + ".msa.embedding_layer.bias");
         m.wp = W(h, tp + ".msa.linear.weight"); m.bp = W(h, tp + ".msa.linear.bias"); m.tab = h->tab[p];
         m.t = t; m.nwh = H / 8; m.nww = Wd / 8; m.H = H; m.W = Wd; m.shift = shift; m.scale = h->scale;
+        if (mlp_in_msa) {
+            m.ln2_g = W(h, tp + ".ln2.weight"); m.ln2_b = W(h, tp + ".ln2.bias");
+            m.w0 = W(h, tp + ".mlp.0.weight"); m.b0 = W(h, tp + ".mlp.0.bias");
+            m.w2 = W(h, tp + ".mlp.2.weight"); m.b2 = W(h, tp + ".mlp.2.bias");
+        }
         const double nw = double(m.nwh) * m.nww;
-        Span sp(h, "msa_fused", 64.0 * nw * (8.0 * t * t) + 16384.0 * t * nw, 4.0 * (2.0 * P * t + 4.0 * t * t));
+        const double msa_flop = 64.0 * nw * (8.0 * t * t) + 16384.0 * t * nw;
+        Span sp(h, mlp_in_msa ? "tblock_fused" : "msa_fused", msa_flop + (mlp_in_msa ? mlp_flop : 0.0),
+                4.0 * (2.0 * P * t + 4.0 * t * t + (mlp_in_msa ? 8.0 * t * t : 0.0)));
         const char* why = nullptr;
         if (!msa_fused(m, h->stream, &why)) return fail(h, why);
         if (!launched(h, "msa_fused")) return false;
     } else if (!msa_unfused(h, p, yt, c, t, H, Wd, shift, s)) {
         return false;
     }
-    {
+    if (!mlp_in_msa) {
         MlpArgs m;
         m.x = yt; m.ldx = c; m.ln_g = W(h, tp + ".ln2.weight"); m.ln_b = W(h, tp + ".ln2.bias");
         m.w0 = W(h, tp + ".mlp.0.weight"); m.b0 = W(h, tp + ".mlp.0.bias");
         m.w2 = W(h, tp + ".mlp.2.weight"); m.b2 = W(h, tp + ".mlp.2.bias"); m.M = P; m.t = t;
-        Span sp(h, "mlp_fused", 16.0 * double(P) * t * t, 4.0 * (2.0 * P * t + 8.0 * t * t + 5.0 * t));
+        Span sp(h, "mlp_fused", mlp_flop, 4.0 * (2.0 * P * t + 8.0 * t * t + 5.0 * t));
         const char* why = nullptr;
         if (!mlp(m, h->stream, &why)) return fail(h, why);
         if (!launched(h, "mlp")) return false;
@@ -592,6 +603,7 @@ int scunet_hip_create(const char* path, scunet_hip** out) {
     // A/B switch: the direct implicit-GEMM 3x3 kernel instead of Winograd F(2x2,3x3).
     h->direct3x3 = std::getenv("SCUNET_HIP_DIRECT3X3") != nullptr;
     h->gemm1x1 = std::getenv("SCUNET_HIP_GEMM1X1") != nullptr;
+    h->separate_mlp = std::getenv("SCUNET_HIP_SEPARATE_MLP") != nullptr;
     if (!upload_weights(h.get())) {
         g_create_error = h->err;
         return 1;

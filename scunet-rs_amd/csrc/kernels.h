@@ -138,11 +138,20 @@ struct MsaArgs {
     const float* wp = nullptr;     // [t][t]
     const float* bp = nullptr;     // [t]
     const float* tab = nullptr;    // [heads][64][64] lane-ordered rel-pos bias
+    // Optional: the MLP with its pre-norm and residual (as MlpArgs), applied to the
+    // window's tokens after the attention residual, in the same kernel (w0 != null).
+    const float* ln2_g = nullptr;
+    const float* ln2_b = nullptr;
+    const float* w0 = nullptr;     // [4t][t]
+    const float* b0 = nullptr;
+    const float* w2 = nullptr;     // [t][4t]
+    const float* b2 = nullptr;
     int t = 0;
     int nwh = 0, nww = 0, H = 0, W = 0, shift = 0;
     float scale = 0.f;
 };
-// t = 32 or 64 (the full-resolution and half-resolution stages); false otherwise.
+// t = 32 or 64 (the full-resolution and half-resolution stages); false otherwise. The MLP
+// option is available at t = 32.
 bool msa_fused(const MsaArgs& a, hipStream_t s, const char** why);
 // Host-side construction of the lane-ordered bias table from rp [heads][15][15].
 void build_bias_table(const float* rp, int heads, float* tab);

@@ -521,7 +521,7 @@ bool gemm(const GemmArgs& g, GemmA a, GemmE e, hipStream_t s, const char** why) 
 // M rows), which leaves each lane holding 4 consecutive output channels of one pixel:
 // a float4 store, and, when chaining, exactly the pixel operand of the next product.
 // ---------------------------------------------------------------------------
-template <int C, int MT, int NW, int MODE>
+template <int C, int MT, int NW, int MODE, bool RPRE>
 __global__ __launch_bounds__(NW * 64) void k_pconv(PconvArgs a) {
     constexpr int NT = C / 16, KG = C / 16, LDW = C + 8;
     constexpr int NMAT = MODE == PC_CHAIN ? 2 : 1;
@@ -568,20 +568,29 @@ __global__ __launch_bounds__(NW * 64) void k_pconv(PconvArgs a) {
         }
     };
 
-    // One group: its rows are in `cur`; the group one stride ahead is loaded into `nxt`
-    // before the product, so that load overlaps this group's MFMAs and stores.
-    auto body = [&](long g, const f4 (&cur)[MT][KG], f4 (&nxt)[MT][KG]) {
-        f4 r[MT][NT];
+    // The residual rows of a group: loaded with its A rows one group ahead (RPRE), or at
+    // the start of the group's own products.
+    auto rload = [&](long g, f4 (&dst)[MT][NT]) {
         if constexpr (MODE != PC_STORE) {
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt) {
                 const long row = g * 16 * MT + mt * 16 + li;
 #pragma unroll
                 for (int nt = 0; nt < NT; ++nt)
-                    r[mt][nt] = row < a.M ? ld4(a.R + row * C + nt * 16 + lg * 4) : f4{0.f, 0.f, 0.f, 0.f};
+                    dst[mt][nt] = row < a.M ? ld4(a.R + row * C + nt * 16 + lg * 4) : f4{0.f, 0.f, 0.f, 0.f};
             }
         }
-        if (g + stride < groups) load(g + stride, nxt);
+    };
+    // One group: its rows are in `cur` (and its residual rows in `rc`); the group one
+    // stride ahead is loaded into `nxt` / `rn` before the product, so those loads overlap
+    // this group's MFMAs and stores.
+    auto body = [&](long g, const f4 (&cur)[MT][KG], f4 (&nxt)[MT][KG], const f4 (&rc)[MT][NT],
+                    f4 (&rn)[MT][NT]) {
+        if constexpr (!RPRE) rload(g, rn);
+        if (g + stride < groups) {
+            load(g + stride, nxt);
+            if constexpr (RPRE) rload(g + stride, rn);
+        }
         // The weights are loop-invariant; an opaque zero offset keeps the compiler from
         // hoisting every LDS weight read out of the loop into registers.
         int wz = 0;
@@ -595,7 +604,7 @@ __global__ __launch_bounds__(NW * 64) void k_pconv(PconvArgs a) {
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt) {
                 acc[mt][nt] = acc[mt][nt] + bv;
-                if constexpr (MODE != PC_STORE) acc[mt][nt] = r[mt][nt] + acc[mt][nt];
+                if constexpr (MODE != PC_STORE) acc[mt][nt] = (RPRE ? rc[mt][nt] : rn[mt][nt]) + acc[mt][nt];
                 const long row = g * 16 * MT + mt * 16 + li;
                 if (row < a.M) st4(a.C + row * C + nt * 16 + lg * 4, acc[mt][nt]);
             }
@@ -616,24 +625,28 @@ __global__ __launch_bounds__(NW * 64) void k_pconv(PconvArgs a) {
     };
 
     f4 xa[MT][KG], xb[MT][KG];
-    if (gi < groups) load(gi, xa);
+    f4 ra[MT][NT], rb[MT][NT];   // unused (and eliminated) without a residual
+    if (gi < groups) {
+        load(gi, xa);
+        if constexpr (RPRE) rload(gi, ra);
+    }
     while (gi < groups) {
-        body(gi, xa, xb);
+        body(gi, xa, xb, ra, rb);
         gi += stride;
         if (gi >= groups) break;
-        body(gi, xb, xa);
+        body(gi, xb, xa, rb, ra);
         gi += stride;
     }
 }
 
-template <int C, int MT, int NW, int MODE>
+template <int C, int MT, int NW, int MODE, bool RPRE>
 static bool launch_pconv(const PconvArgs& a, hipStream_t s) {
     static int per_cu = -1, cus = 0;
     if (per_cu < 0) {
         int dev = 0;
         if (hipGetDevice(&dev) != hipSuccess) return false;
         if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return false;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_pconv<C, MT, NW, MODE>, NW * 64, 0) !=
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_pconv<C, MT, NW, MODE, RPRE>, NW * 64, 0) !=
             hipSuccess)
             return false;
         if (per_cu < 1) per_cu = 1;
@@ -641,7 +654,7 @@ static bool launch_pconv(const PconvArgs& a, hipStream_t s) {
     const long groups = (a.M + 16 * MT - 1) / (16 * MT);
     const long waves = std::min<long>(groups, long(cus) * per_cu * NW);
     dim3 grid{unsigned((waves + NW - 1) / NW), 1u, 1u}, block{unsigned(NW * 64), 1u, 1u};
-    hipLaunchKernelGGL((k_pconv<C, MT, NW, MODE>), grid, block, 0, s, a);
+    hipLaunchKernelGGL((k_pconv<C, MT, NW, MODE, RPRE>), grid, block, 0, s, a);
     return true;
 }
 
@@ -651,13 +664,13 @@ bool pconv(const PconvArgs& a, PconvMode mode, hipStream_t s, const char** why) 
     if (a.M <= 0) return true;
     bool ok = false;
     if (a.c == 64) {
-        if (mode == PC_STORE) ok = launch_pconv<64, 2, 4, PC_STORE>(a, s);
-        else if (mode == PC_RESID) ok = launch_pconv<64, 2, 4, PC_RESID>(a, s);
-        else ok = launch_pconv<64, 2, 4, PC_CHAIN>(a, s);
+        if (mode == PC_STORE) ok = launch_pconv<64, 2, 4, PC_STORE, false>(a, s);
+        else if (mode == PC_RESID) ok = launch_pconv<64, 2, 4, PC_RESID, false>(a, s);
+        else ok = launch_pconv<64, 2, 4, PC_CHAIN, false>(a, s);
     } else if (a.c == 128) {
-        if (mode == PC_STORE) ok = launch_pconv<128, 1, 4, PC_STORE>(a, s);
-        else if (mode == PC_RESID) ok = launch_pconv<128, 1, 4, PC_RESID>(a, s);
-        else ok = launch_pconv<128, 1, 8, PC_CHAIN>(a, s);
+        if (mode == PC_STORE) ok = launch_pconv<128, 1, 4, PC_STORE, false>(a, s);
+        else if (mode == PC_RESID) ok = launch_pconv<128, 1, 4, PC_RESID, false>(a, s);
+        else ok = launch_pconv<128, 1, 8, PC_CHAIN, false>(a, s);
     } else {
         *why = "pconv: only 64 or 128 channels have a resident-weight configuration";
         return false;
@@ -1025,26 +1038,36 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int tx = (a.W + 15) >> 4, nb = a.cout / 16, nch = a.cin / BK;
     const int tr = 2 * wave + (li >> 3), tc = li & 7;
 
-    f4 rh[HV], ru[UV];
-    auto load = [&](const WinoUnit& w, int ci0) {
+    // Load addressing: 32-bit element offsets per lane, fixed per kernel (U) or per unit
+    // (halo); a slice only adds its uniform channel base, so the loop does no address
+    // arithmetic. A plane of P pixels x ldi channels must have P * ldi < 2^32 (checked by
+    // the launcher). NOFF marks a halo position outside the image: it loads zeros.
+    constexpr unsigned NOFF = 0xffffffffu;
+    unsigned uoff[UV];
+#pragma unroll
+    for (int i = 0; i < UV; ++i) {
+        const int f = tid + i * 256;
+        const int xi = f >> 6, rem = f & 63, co = rem >> 2, c4 = rem & 3;
+        uoff[i] = (unsigned(xi) * unsigned(a.cout) + unsigned(co)) * unsigned(a.cin) + unsigned(c4 * 4);
+    }
+    auto halo_offsets = [&](const WinoUnit& w, unsigned (&ho)[HV]) {
 #pragma unroll
         for (int i = 0; i < HV; ++i) {
             const int f = tid + i * 256;
-            f4 v = {0.f, 0.f, 0.f, 0.f};
-            if (f < HW * HW * 4 && w.y0 >= 0) {
-                const int px = f >> 2, c4 = f & 3;
-                const int gy = w.y0 - 1 + px / HW, gx = w.x0 - 1 + px % HW;
-                if (gy >= 0 && gy < a.H && gx >= 0 && gx < a.W)
-                    v = ld4(a.in + (long(gy) * a.W + gx) * a.ldi + ci0 + c4 * 4);
-            }
-            rh[i] = v;
+            const int px = f >> 2, c4 = f & 3;
+            const int gy = w.y0 - 1 + px / HW, gx = w.x0 - 1 + px % HW;
+            const bool ok = f < HW * HW * 4 && w.y0 >= 0 && gy >= 0 && gy < a.H && gx >= 0 && gx < a.W;
+            ho[i] = ok ? (unsigned(gy) * unsigned(a.W) + unsigned(gx)) * unsigned(a.ldi) + unsigned(c4 * 4) : NOFF;
         }
+    };
+    f4 rh[HV], ru[UV];
+    auto load = [&](const unsigned (&ho)[HV], int co0, int ci0) {
+        const float* hb = a.in + ci0;
 #pragma unroll
-        for (int i = 0; i < UV; ++i) {
-            const int f = tid + i * 256;
-            const int xi = f >> 6, rem = f & 63, co = rem >> 2, c4 = rem & 3;
-            ru[i] = ld4(a.w + (long(xi) * a.cout + w.co0 + co) * a.cin + ci0 + c4 * 4);
-        }
+        for (int i = 0; i < HV; ++i) rh[i] = ho[i] != NOFF ? ld4(hb + ho[i]) : f4{0.f, 0.f, 0.f, 0.f};
+        const float* ub = a.w + long(co0) * a.cin + ci0;
+#pragma unroll
+        for (int i = 0; i < UV; ++i) ru[i] = ld4(ub + uoff[i]);
     };
     auto stash = [&]() {
 #pragma unroll
@@ -1065,19 +1088,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     long u = blockIdx.x;
     if (u >= units) return;
     WinoUnit cur = wino_unit(u, tx, nb, tiles);
-    load(cur, 0);
+    unsigned hcur[HV], hnxt[HV];
+    halo_offsets(cur, hcur);
+    load(hcur, cur.co0, 0);
     for (;;) {
         f4 acc[16];
 #pragma unroll
         for (int xi = 0; xi < 16; ++xi) acc[xi] = f4{0.f, 0.f, 0.f, 0.f};
         const long un = u + gridDim.x;
         const WinoUnit nxt = wino_unit(un, tx, nb, tiles);
+        halo_offsets(nxt, hnxt);
         for (int c = 0; c < nch; ++c) {
             __syncthreads();
             stash();
             __syncthreads();
-            if (c + 1 < nch) load(cur, (c + 1) * BK);
-            else if (un < units) load(nxt, 0);
+            if (c + 1 < nch) load(hcur, cur.co0, (c + 1) * BK);
+            else if (un < units) load(hnxt, nxt.co0, 0);
             // T = B^T d column by column (each needs one column of the patch), then row i
             // of V = T B feeds the products for xi = 4i .. 4i+3 (channels 4lg .. 4lg+3).
             f4 t[4][4];
@@ -1135,12 +1161,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         if (un >= units) break;
         u = un;
         cur = nxt;
+#pragma unroll
+        for (int i = 0; i < HV; ++i) hcur[i] = hnxt[i];
     }
 }
 
 bool conv3x3_winograd(const Conv3Args& a, bool relu, hipStream_t s, const char** why) {
     if (a.cin % 16 != 0 || a.cout % 16 != 0 || (a.H & 1) || (a.W & 1)) {
         *why = "conv3x3_winograd: cin and cout must be multiples of 16 and the plane even";
+        return false;
+    }
+    if (double(a.H) * a.W * a.ldi >= 4294967296.0 || double(a.cout) * a.cin * 16 >= 4294967296.0) {
+        *why = "conv3x3_winograd: plane too large for 32-bit element offsets";
         return false;
     }
     static int per_cu[2] = {-1, -1}, cus = 0;
@@ -1328,11 +1360,27 @@ bool attention(const AttnArgs& a, hipStream_t s, const char** why) {
 //   3. x += out + bias, written back through the same index map (a permutation, so each
 //      window owns its 64 rows).
 // ---------------------------------------------------------------------------
-template <int T>
-__global__ __launch_bounds__(256) void k_msa(MsaArgs a, long nw) {
+template <int T, bool MLP>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(T == 32 ? 2 : 1, 2))) void k_msa(MsaArgs a, long nw) {
     constexpr int HEADS = T / 32, KG = T / 16, OT = T / 16, LDX = T + 4;
-    __shared__ float xs[4 * 64 * LDX];
+    // MLP weights, resident for the whole workgroup: W0 [4T][T] and W2 [T][4T] with row
+    // pitches T + 8 and 4T + 8 (conflict-free operand reads).
+    constexpr int HID = 4 * T, P0 = T + 8, P2 = HID + 8;
+    constexpr int MLPF = MLP ? HID * P0 + T * P2 : 0;
+    __shared__ float xs[4 * 64 * LDX + MLPF];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    float* const wm0 = xs + 4 * 64 * LDX;
+    float* const wm2 = wm0 + HID * P0;
+    if constexpr (MLP) {
+        for (int f = threadIdx.x; f < HID * T / 4; f += 256) {
+            const int r = f / (T / 4), c4 = f % (T / 4);
+            st4(wm0 + r * P0 + c4 * 4, ld4(a.w0 + long(r) * T + c4 * 4));
+        }
+        for (int f = threadIdx.x; f < T * HID / 4; f += 256) {
+            const int r = f / (HID / 4), c4 = f % (HID / 4);
+            st4(wm2 + r * P2 + c4 * 4, ld4(a.w2 + long(r) * HID + c4 * 4));
+        }
+    }
     const int li = lane & 15, lg = lane >> 4;
     const long wi = long(blockIdx.x) * 4 + wave;
     const bool valid = wi < nw;
@@ -1495,14 +1543,96 @@ __global__ __launch_bounds__(256) void k_msa(MsaArgs a, long nw) {
         }
     }
     // 3. Residual: lanes hold outputs 16ot + 4lg .. +3 of token 16nt + li.
+    f4 xr[4][OT];
 #pragma unroll
     for (int nt = 0; nt < 4; ++nt) {
         const long row = rowof(nt * 16 + li);
 #pragma unroll
-        for (int ot = 0; ot < OT; ++ot) {
-            float* o = a.x + row * a.ldx + ot * 16 + lg * 4;
-            st4(o, ld4(o) + (acc[nt][ot] + ld4(a.bp + ot * 16 + lg * 4)));
+        for (int ot = 0; ot < OT; ++ot)
+            xr[nt][ot] = ld4(a.x + row * a.ldx + ot * 16 + lg * 4) + (acc[nt][ot] + ld4(a.bp + ot * 16 + lg * 4));
+    }
+    if constexpr (MLP) {
+        // 4. The MLP on the window's tokens (cpu.rs:800-860), exactly as k_mlp computes it:
+        // LN2 in registers, the hidden layer produced 32 units at a time transposed (so it
+        // is directly the second product's operand), GELU, and the second residual.
+        constexpr int HC = 32, HT = HC / 16;
+        f4 xn[4][OT];
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+            float sm = 0.f;
+#pragma unroll
+            for (int kg = 0; kg < OT; ++kg) sm += (xr[mt][kg].x + xr[mt][kg].y) + (xr[mt][kg].z + xr[mt][kg].w);
+            sm += __shfl_xor(sm, 16);
+            sm += __shfl_xor(sm, 32);
+            const float mu = sm / float(T);
+            float q = 0.f;
+#pragma unroll
+            for (int kg = 0; kg < OT; ++kg) {
+                f4 d = xr[mt][kg] - mu;
+                q += (d.x * d.x + d.y * d.y) + (d.z * d.z + d.w * d.w);
+            }
+            q += __shfl_xor(q, 16);
+            q += __shfl_xor(q, 32);
+            const float rs = 1.0f / sqrtf(q / float(T) + 1e-5f);
+#pragma unroll
+            for (int kg = 0; kg < OT; ++kg) {
+                f4 gg = ld4(a.ln2_g + kg * 16 + lg * 4), bb = ld4(a.ln2_b + kg * 16 + lg * 4);
+                xn[mt][kg] = (xr[mt][kg] - mu) * rs * gg + bb;
+            }
         }
+        f4 acc2[4][OT];
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+            for (int nt = 0; nt < OT; ++nt) acc2[mt][nt] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll 1
+        for (int ch = 0; ch < HID / HC; ++ch) {
+            f4 acc1[HT][4];
+#pragma unroll
+            for (int ht = 0; ht < HT; ++ht)
+#pragma unroll
+                for (int mt = 0; mt < 4; ++mt) acc1[ht][mt] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int kg = 0; kg < OT; ++kg)
+#pragma unroll
+                for (int ht = 0; ht < HT; ++ht) {
+                    const f4 wv = ld4(wm0 + (ch * HC + ht * 16 + li) * P0 + kg * 16 + lg * 4);
+#pragma unroll
+                    for (int s4 = 0; s4 < 4; ++s4)
+#pragma unroll
+                        for (int mt = 0; mt < 4; ++mt) acc1[ht][mt] = mfma4(wv[s4], xn[mt][kg][s4], acc1[ht][mt]);
+                }
+#pragma unroll
+            for (int ht = 0; ht < HT; ++ht) {
+                const f4 bb = ld4(a.b0 + ch * HC + ht * 16 + lg * 4);
+#pragma unroll
+                for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) acc1[ht][mt][r] = gelu_as(acc1[ht][mt][r] + bb[r]);
+            }
+#pragma unroll
+            for (int ht = 0; ht < HT; ++ht)
+#pragma unroll
+                for (int nt = 0; nt < OT; ++nt) {
+                    const f4 wv = ld4(wm2 + (nt * 16 + li) * P2 + ch * HC + ht * 16 + lg * 4);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+#pragma unroll
+                        for (int mt = 0; mt < 4; ++mt) acc2[mt][nt] = mfma4(wv[r], acc1[ht][mt][r], acc2[mt][nt]);
+                }
+        }
+#pragma unroll
+        for (int nt = 0; nt < OT; ++nt) {
+            const f4 bv = ld4(a.b2 + nt * 16 + lg * 4);
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt) xr[mt][nt] = xr[mt][nt] + (acc2[mt][nt] + bv);
+        }
+    }
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) {
+        const long row = rowof(nt * 16 + li);
+#pragma unroll
+        for (int ot = 0; ot < OT; ++ot) st4(a.x + row * a.ldx + ot * 16 + lg * 4, xr[nt][ot]);
     }
 }
 
@@ -1510,8 +1640,13 @@ bool msa_fused(const MsaArgs& a, hipStream_t s, const char** why) {
     const long nw = long(a.nwh) * a.nww;
     if (nw == 0) return true;
     dim3 grid{unsigned((nw + 3) / 4), 1u, 1u}, block{256u, 1u, 1u};
-    if (a.t == 32) hipLaunchKernelGGL(k_msa<32>, grid, block, 0, s, a, nw);
-    else if (a.t == 64) hipLaunchKernelGGL(k_msa<64>, grid, block, 0, s, a, nw);
+    if (a.w0 && a.t != 32) {
+        *why = "msa_fused: the fused MLP is available at t = 32 only";
+        return false;
+    }
+    if (a.t == 32 && a.w0) hipLaunchKernelGGL((k_msa<32, true>), grid, block, 0, s, a, nw);
+    else if (a.t == 32) hipLaunchKernelGGL((k_msa<32, false>), grid, block, 0, s, a, nw);
+    else if (a.t == 64) hipLaunchKernelGGL((k_msa<64, false>), grid, block, 0, s, a, nw);
     else {
         *why = "msa_fused: t must be 32 or 64";
         return false;

@@ -209,3 +209,32 @@ def test_resident_chained_1x1_and_tiled_gemm_agree(weights_path, owt):
     finally:
         chained.close()
         tiled.close()
+
+
+def test_mlp_inside_window_kernel_and_separate_mlp_agree(weights_path, owt, weights_path_affine):
+    """At t = 32 the MLP (LN2, mlp.0, GELU, mlp.2, residual; cpu.rs:800-860) runs inside the
+    window-attention kernel on each window's tokens (the default) or as its own kernel
+    (SCUNET_HIP_SEPARATE_MLP): both against the oracle's block, unshifted and shifted, on the
+    identity-LN checkpoint and on one with random LayerNorm affines."""
+    from scunet_hip import Hip, synth
+    for wpath in (weights_path, weights_path_affine):
+        ow = owt if wpath == weights_path else O.Weights.load(wpath)
+        os.environ["SCUNET_HIP_SEPARATE_MLP"] = "1"
+        try:
+            sep = Hip(wpath)
+        finally:
+            del os.environ["SCUNET_HIP_SEPARATE_MLP"]
+        fused = Hip(wpath)
+        try:
+            for prefix, shift, (h, w) in (("m_down1.0", 0, (24, 40)), ("m_down1.1", 4, (32, 24)),
+                                          ("m_up1.3", 0, (16, 16)), ("m_up1.4", 4, (40, 48))):
+                c = sum(ow.block_dims(prefix))
+                x = synth.seq(c * h * w, 0.53).reshape(c, h, w)
+                want = O.conv_trans_block(ow, prefix, x, shift)
+                a = fused.block_dump(prefix, h, w, shift, x)
+                b = sep.block_dump(prefix, h, w, shift, x)
+                assert max_abs(want, a) <= STAGE_TOL, (wpath, prefix, "fused")
+                assert max_abs(want, b) <= STAGE_TOL, (wpath, prefix, "separate")
+        finally:
+            fused.close()
+            sep.close()
