@@ -53,6 +53,7 @@ struct scunet_hip {
     size_t wbytes = 0;
     std::map<std::string, float*> w;
     std::map<std::string, float*> tab;   // block prefix -> lane-ordered rel-pos bias table
+    std::map<std::string, float*> atab;  // block prefix -> the attention kernel's 4-variant table
 
     // Arena: role -> (pointer, bytes), grown on demand, kept across calls.
     std::map<std::string, std::pair<float*, size_t>> arena;
@@ -197,6 +198,9 @@ bool upload_weights(scunet_hip* h) {
             build_bias_table(t.data, heads, tab.data());
             std::string prefix = n.substr(0, n.find(".trans_block"));
             host.push_back({"@tab:" + prefix, std::move(tab)});
+            std::vector<float> atab(size_t(heads) * 225);
+            build_attn_table(t.data, heads, atab.data());
+            host.push_back({"@atab:" + prefix, std::move(atab)});
         }
         host.push_back({n, std::move(v)});
     }
@@ -211,6 +215,7 @@ bool upload_weights(scunet_hip* h) {
         if (!ck(h, hipMemcpy(at, e.second.data(), e.second.size() * 4, hipMemcpyHostToDevice), "weight upload"))
             return false;
         if (e.first.rfind("@tab:", 0) == 0) h->tab[e.first.substr(5)] = reinterpret_cast<float*>(at);
+        else if (e.first.rfind("@atab:", 0) == 0) h->atab[e.first.substr(6)] = reinterpret_cast<float*>(at);
         else h->w[e.first] = reinterpret_cast<float*>(at);   // "@wino:<name>" are Winograd filters
         at += (e.second.size() * 4 + 255) / 256 * 256;
     }
@@ -278,7 +283,7 @@ bool msa_unfused(scunet_hip* h, const std::string& p, float* yt, int c, int t, i
     if (!run_gemm(h, "qkv_ln", g, A_LN, E_STORE)) return false;
     {
         AttnArgs a;
-        a.qkv = s.qkv; a.ldq = 3 * t; a.out = s.o; a.ldo = t; a.tab = h->tab[p];
+        a.qkv = s.qkv; a.ldq = 3 * t; a.out = s.o; a.ldo = t; a.tab = h->atab[p];
         a.C = t; a.heads = t / h->wt.head_dim; a.nwh = H / 8; a.nww = Wd / 8; a.H = H; a.W = Wd;
         a.shift = shift; a.pixel_mode = 1; a.scale = h->scale;
         long nw = long(a.nwh) * a.nww;
@@ -925,8 +930,8 @@ int scunet_hip_attention_kernel_probe(scunet_hip* h, size_t hh, size_t ww, size_
         size_t nw = (hh / 8) * (ww / 8), nt = nw * 64;
         float *dq, *dt;
         if (!to_device(h, "probe_in", qkv, nt * 3 * c, &dq)) return false;
-        std::vector<float> tab(heads * 64 * 64);
-        build_bias_table(rp, int(heads), tab.data());
+        std::vector<float> tab(heads * 225);
+        build_attn_table(rp, int(heads), tab.data());
         if (!to_device(h, "probe_tab", tab.data(), tab.size(), &dt)) return false;
         float* y = buf(h, "probe_out", nt * c);
         if (!y) return false;
@@ -1001,7 +1006,7 @@ int scunet_hip_attention_probe(scunet_hip* h, const char* prefix, size_t hh, siz
         g.C = qkv; g.ldc = 3 * t; g.M = P; g.N = 3 * t; g.K = t;
         if (!run_gemm(h, "qkv_ln", g, A_LN, E_STORE)) return false;
         AttnArgs a;
-        a.qkv = qkv; a.ldq = 3 * t; a.out = att; a.ldo = t; a.tab = h->tab[prefix]; a.C = t;
+        a.qkv = qkv; a.ldq = 3 * t; a.out = att; a.ldo = t; a.tab = h->atab[prefix]; a.C = t;
         a.heads = t / h->wt.head_dim; a.nwh = int(hh / 8); a.nww = int(ww / 8); a.H = int(hh); a.W = int(ww);
         a.shift = int(shift); a.pixel_mode = 1; a.scale = h->scale;
         const char* why = nullptr;
@@ -1020,8 +1025,8 @@ int scunet_hip_bench_attn(scunet_hip* h, const float* qkv, const float* rp, floa
                           size_t c, size_t heads, size_t shift, int iters, double* ms) {
     return guard(h, [&] {
         if (c != heads * 32) return fail(h, "the attention kernel needs head_dim 32");
-        std::vector<float> tab(heads * 64 * 64);
-        build_bias_table(rp, int(heads), tab.data());
+        std::vector<float> tab(heads * 225);
+        build_attn_table(rp, int(heads), tab.data());
         float* dt;
         if (!to_device(h, "bench_tab", tab.data(), tab.size(), &dt)) return false;
         AttnArgs a;

@@ -114,7 +114,7 @@ struct AttnArgs {
     long ldq = 0;
     float* out = nullptr;          // rows of C
     long ldo = 0;
-    const float* tab = nullptr;    // [heads][64 lanes][64] rel-pos bias in lane order
+    const float* tab = nullptr;    // [heads][15][15] from build_attn_table
     int C = 0, heads = 0;
     int nwh = 0, nww = 0;          // window grid
     int H = 0, W = 0;              // plane (pixel mode)
@@ -122,7 +122,7 @@ struct AttnArgs {
     int pixel_mode = 1;            // 1: rows are pixels y*W+x; 0: rows are window*64+token
     float scale = 0.f;
 };
-// 8x8 windows, head_dim 32 only.
+// 8x8 windows, head_dim 32, at most 8 heads.
 bool attention(const AttnArgs& a, hipStream_t s, const char** why);
 
 // The whole window-attention half of a Swin block, fused per window (cpu.rs:791-799):
@@ -155,6 +155,8 @@ struct MsaArgs {
 bool msa_fused(const MsaArgs& a, hipStream_t s, const char** why);
 // Host-side construction of the lane-ordered bias table from rp [heads][15][15].
 void build_bias_table(const float* rp, int heads, float* tab);
+// The attention kernel's table: rp [heads][15][15] scaled by log2(e).
+void build_attn_table(const float* rp, int heads, float* tab);
 
 // m_head (in_nc -> dim, 3x3, zero pad) reading an NCHW image of size hh x ww that is
 // replicate-padded on the fly to H x W; writes (or, with add, accumulates into) the

@@ -1220,92 +1220,124 @@ void winograd_filter(const float* g, int cout, int cin, float* u) {
 //   S^T = K Q^T on MFMA (keys are the M rows, queries the N columns), so after the
 //   product each lane holds, for ONE query, 16 of its 64 key logits; the other 48
 //   are in the lanes 16, 32 and 48 away. Softmax: max and sum over the 16 values and a
-//   two-step xor shuffle. The probabilities are then exactly the A operand of
-//   O = P V (lane = query row, registers = 4 consecutive keys of the lane's key group),
-//   so no data moves between the two products and nothing goes through LDS.
-// Logit = (q.k) * scale + bias[h][p][q]; masked -> -FLT_MAX/4 (cpu.rs:365-370, 681-683).
+//   two-step xor shuffle. The exponentials are then exactly the B operand of
+//   O^T = V^T P^T (lane = query, registers = 4 consecutive keys of the lane's key group),
+//   so no data moves between the two products and nothing goes through LDS; the 1/sum
+//   normalisation is applied to the 8 outputs rather than the 16 weights.
+// Logits are kept in log2 units, l = (q.k) * scale * log2(e) + log2(e) * bias, so a logit is
+// one FMA and softmax uses 2^(l - max); masked logits are -FLT_MAX/4 (cpu.rs:365-370,
+// 681-683). The per-head 15x15 bias tables sit in LDS; each lane reads the 28 entries its
+// 64 logits use. V is transposed through a per-wave LDS slice so that every global load is
+// a 16-byte row load.
 // ---------------------------------------------------------------------------
-DEVI long win_row(const AttnArgs& a, long wi, int t, int wh, int ww) {
-    if (!a.pixel_mode) return wi * 64 + t;
-    int y = wh * 8 + (t >> 3) + a.shift;
-    int x = ww * 8 + (t & 7) + a.shift;
-    if (y >= a.H) y -= a.H;
-    if (x >= a.W) x -= a.W;
-    return long(y) * a.W + x;
-}
-
-__global__ __launch_bounds__(256) void k_attention(AttnArgs a, long units) {
-    const int lane = threadIdx.x & 63;
-    const long u = long(blockIdx.x) * 4 + (threadIdx.x >> 6);
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) void k_attention(AttnArgs a, long units) {
+    constexpr int VP = 72;                        // V^T row pitch (conflict-free b128 reads)
+    __shared__ float rps[8 * 225];                // log2(e) * rel-pos tables, all heads
+    __shared__ float vts[4][32 * VP];             // per wave: V^T [dim][key]
+    for (int i = threadIdx.x; i < a.heads * 225; i += 256) rps[i] = a.tab[i];
+    __syncthreads();                              // the only barrier
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const long u = long(blockIdx.x) * 4 + wave;
     if (u >= units) return;                      // whole wave exits together
     const int li = lane & 15, lg = lane >> 4;
     const long wi = u / a.heads;
     const int h = int(u - wi * a.heads);
     const int wh = int(wi / a.nww), ww = int(wi - long(wh) * a.nww);
     const int hoff = h * 32;
+
+    // Element offsets of the rows of tokens 16m + li (Q, K, V and the output). In pixel
+    // mode token (ty, tx) of window (wh, ww) is pixel ((8wh + ty + shift) mod H,
+    // (8ww + tx + shift) mod W) (cpu.rs:648-652's cyclic shift folded into the
+    // addressing); the launcher checks that every offset fits 32 bits.
+    unsigned off[4];
+    if (a.pixel_mode) {
+        auto wy = [&](int ty) { int y = wh * 8 + ty + a.shift; return unsigned(y >= a.H ? y - a.H : y); };
+        int x = ww * 8 + (li & 7) + a.shift;
+        const unsigned xq = unsigned(x >= a.W ? x - a.W : x);
+#pragma unroll
+        for (int m = 0; m < 4; ++m) off[m] = (wy(2 * m + (li >> 3)) * unsigned(a.W) + xq) * unsigned(a.ldq);
+    } else {
+#pragma unroll
+        for (int m = 0; m < 4; ++m) off[m] = (unsigned(wi) * 64u + 16u * m + li) * unsigned(a.ldq);
+    }
     const float* q_base = a.qkv + hoff;
     const float* k_base = a.qkv + a.C + hoff;
     const float* v_base = a.qkv + 2 * a.C + hoff;
 
-    // K fragments: key tile mt (rows 16mt + li), dim group G (dims 16G + 4lg .. +3).
-    f4 kf[4][2];
+    // All of the window-head's operands are requested before the first product.
+    // Q / K / V rows: token 16m + li, dim group G (dims 16G + 4lg .. +3).
+    f4 kf[4][2], qf[4][2], vr[4][2];
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
-        long row = win_row(a, wi, mt * 16 + li, wh, ww);
+    for (int m = 0; m < 4; ++m)
 #pragma unroll
-        for (int G = 0; G < 2; ++G) kf[mt][G] = ld4(k_base + row * a.ldq + G * 16 + lg * 4);
-    }
-    // V as the B operand of P V: key 16kt + 4lg + r, dim 16nd + li.
-    float vv[4][4][2];
+        for (int G = 0; G < 2; ++G) {
+            kf[m][G] = ld4(k_base + off[m] + G * 16 + lg * 4);
+            qf[m][G] = ld4(q_base + off[m] + G * 16 + lg * 4);
+            vr[m][G] = ld4(v_base + off[m] + G * 16 + lg * 4);
+        }
+    // Bias: query p = 16nt + li and key q = 16mt + 4lg + r give table entry
+    // (p/8 - q/8 + 7) * 15 + (p%8 - q%8 + 7) = base + 30 (nt - mt) - r (cpu.rs:532-546),
+    // so a lane needs only the 28 entries base + 30 d - r, d = -3 .. 3.
+    const int base = 15 * ((li >> 3) - (lg >> 1)) + (li & 7) - 4 * (lg & 1) + 112;
+    float bl[7][4];
+#pragma unroll
+    for (int d = 0; d < 7; ++d)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) bl[d][r] = rps[h * 225 + base + 30 * (d - 3) - r];
+    // V^T through this wave's LDS slice: written as rows arrive, read back as the A operand
+    // of O^T = V^T P^T (dim 16nd + li, keys 16kt + 4lg .. +3).
+    float* vt = vts[wave];
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+#pragma unroll
+        for (int G = 0; G < 2; ++G)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) vt[(16 * G + 4 * lg + c) * VP + 16 * m + li] = vr[m][G][c];
+    f4 vv[4][2];
 #pragma unroll
     for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            long row = win_row(a, wi, kt * 16 + lg * 4 + r, wh, ww);
-#pragma unroll
-            for (int nd = 0; nd < 2; ++nd) vv[kt][r][nd] = v_base[row * a.ldq + nd * 16 + li];
-        }
+        for (int nd = 0; nd < 2; ++nd) vv[kt][nd] = ld4(vt + (16 * nd + li) * VP + 16 * kt + 4 * lg);
 
-    const bool masked = a.shift > 0;
-    const bool row_edge = masked && wh == a.nwh - 1;
-    const bool col_edge = masked && ww == a.nww - 1;
-    const float* tab = a.tab + (long(h) * 64 + lane) * 64;
+    // Shifted-window mask (cpu.rs:548-589, 681-683): in the last window row, query and key
+    // on different sides of the row split; in the last window column, on different sides of
+    // the column split. The row part depends on (nt, mt) only, the column part on the lane.
+    const bool row_edge = a.shift > 0 && wh == a.nwh - 1;
+    const bool col_edge = a.shift > 0 && ww == a.nww - 1;
+    const bool col_hit = col_edge && (((li & 7) < 4) != ((lg & 1) == 0));
     const float SENT = -3.4028234663852886e38f / 4.0f;
+    const float sc = a.scale * 1.4426950408889634f;   // logits in log2 units: p = 2^(l - max)
 
 #pragma unroll
     for (int nt = 0; nt < 4; ++nt) {
-        long qrow = win_row(a, wi, nt * 16 + li, wh, ww);
-        f4 qf[2];
-#pragma unroll
-        for (int G = 0; G < 2; ++G) qf[G] = ld4(q_base + qrow * a.ldq + G * 16 + lg * 4);
         f4 S[4];
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt) S[mt] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int G = 0; G < 2; ++G)
 #pragma unroll
-            for (int s = 0; s < 4; ++s)
+            for (int s4 = 0; s4 < 4; ++s4)
 #pragma unroll
-                for (int mt = 0; mt < 4; ++mt) S[mt] = mfma4(kf[mt][G][s], qf[G][s], S[mt]);
+                for (int mt = 0; mt < 4; ++mt) S[mt] = mfma4(kf[mt][G][s4], qf[nt][G][s4], S[mt]);
 
         // Logits for query 16nt + li against keys 16mt + 4lg + r.
-        const bool q_row_lo = nt < 2;
-        const bool q_col_lo = (li & 7) < 4;
-        const bool k_col_lo = (lg & 1) == 0;
-        float mx = -INFINITY;
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
-            f4 b = ld4(tab + nt * 16 + mt * 4);
-            const bool k_row_lo = mt < 2;
-            const bool hit = (row_edge && (q_row_lo != k_row_lo)) || (col_edge && (q_col_lo != k_col_lo));
+        for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                float v = S[mt][r] * a.scale + b[r];
-                if (hit) v = SENT;
-                S[mt][r] = v;
-                mx = fmaxf(mx, v);
+            for (int r = 0; r < 4; ++r) S[mt][r] = fmaf(S[mt][r], sc, bl[nt - mt + 3][r]);
+        if (row_edge || col_edge) {
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt) {
+                const bool hit = (row_edge && ((nt < 2) != (mt < 2))) || col_hit;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) S[mt][r] = hit ? SENT : S[mt][r];
             }
         }
+        float mx = -INFINITY;
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) mx = fmaxf(mx, S[mt][r]);
         mx = fmaxf(mx, __shfl_xor(mx, 16));
         mx = fmaxf(mx, __shfl_xor(mx, 32));
         float sum = 0.0f;
@@ -1313,34 +1345,36 @@ __global__ __launch_bounds__(256) void k_attention(AttnArgs a, long units) {
         for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                float e = __expf(S[mt][r] - mx);
+                const float e = __builtin_amdgcn_exp2f(S[mt][r] - mx);
                 S[mt][r] = e;
                 sum += e;
             }
         sum += __shfl_xor(sum, 16);
         sum += __shfl_xor(sum, 32);
-        const float inv = 1.0f / sum;
 
-        // O^T = V^T P^T: the probabilities are the B operand as they stand (lane = query,
-        // registers = 4 consecutive keys), V the A operand; the result leaves each lane with
-        // 4 consecutive dims of one query: dims 16nd + 4lg .. +3 of query 16nt + li.
+        // O^T = V^T P^T with the unnormalised weights (lane = query, registers = 4
+        // consecutive keys: the B operand as they stand), then O / sum: each lane ends with
+        // dims 16nd + 4lg .. +3 of query 16nt + li.
         f4 O[2] = {f4{0.f, 0.f, 0.f, 0.f}, f4{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
         for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                float p = S[kt][r] * inv;
+            for (int r = 0; r < 4; ++r)
 #pragma unroll
-                for (int nd = 0; nd < 2; ++nd) O[nd] = mfma4(vv[kt][r][nd], p, O[nd]);
-            }
-        float* o = a.out + qrow * a.ldo + hoff + lg * 4;
-        st4(o, O[0]);
-        st4(o + 16, O[1]);
+                for (int nd = 0; nd < 2; ++nd) O[nd] = mfma4(vv[kt][nd][r], S[kt][r], O[nd]);
+        const float inv = 1.0f / sum;
+        float* o = a.out + long(off[nt] / unsigned(a.ldq)) * a.ldo + hoff + lg * 4;
+        st4(o, O[0] * inv);
+        st4(o + 16, O[1] * inv);
     }
 }
 
 bool attention(const AttnArgs& a, hipStream_t s, const char** why) {
     if (a.C != a.heads * 32) { *why = "attention: head_dim must be 32"; return false; }
+    const double rows = a.pixel_mode ? double(a.H) * a.W : double(a.nwh) * a.nww * 64.0;
+    if (rows * double(a.ldq) >= 4294967296.0) { *why = "attention: qkv plane too large for 32-bit offsets"; return false; }
+    if (a.shift != 0 && a.shift != 4) { *why = "attention: the shifted-window mask assumes shift 4"; return false; }
+    if (a.heads > 8) { *why = "attention: at most 8 heads"; return false; }
     long units = long(a.nwh) * a.nww * a.heads;
     if (units == 0) return true;
     dim3 grid(unsigned((units + 3) / 4));
@@ -1667,6 +1701,12 @@ void build_bias_table(const float* rp, int heads, float* tab) {
                         int dy = p / 8 - q / 8 + 7, dx = p % 8 - q % 8 + 7;
                         tab[((long(h) * 64 + lane) * 4 + nt) * 16 + mt * 4 + r] = rp[h * 225 + dy * 15 + dx];
                     }
+}
+
+void build_attn_table(const float* rp, int heads, float* tab) {
+    // tab[h][dy][dx] = log2(e) * rp[h][dy][dx]: the attention kernel keeps logits in log2
+    // units (softmax as 2^(l - max)).
+    for (long i = 0; i < long(heads) * 225; ++i) tab[i] = float(double(rp[i]) * 1.4426950408889634);
 }
 
 // ---------------------------------------------------------------------------
