@@ -59,20 +59,23 @@ def measured_traffic():
         return json.load(f).get("classes", {})
 
 
-def cpu_baseline(weights_path, sample_hw):
-    """The oracle (C++ restatement of the reference's src/cpu.rs) on a bounded sample."""
+def cpu_baseline(weights_path, x, rows):
+    """The oracle (C++ restatement of the reference's src/cpu.rs, OpenMP over all host
+    threads) on a bounded sample of the benchmark's own input: the top `rows` rows of the
+    1080p image, forwarded as a whole image (same per-pixel work)."""
+    import numpy as np
     sys.path.insert(0, os.path.join(REPO, "oracle"))
     import oracle
-    from scunet_hip import synth
     wt = oracle.Weights.load(weights_path)
-    h, w = sample_hw
-    x = synth.noisy_image(102, 3, h, w, 50, "gradient")
+    sample = np.ascontiguousarray(x[:, :rows, :])
+    c, h, w = sample.shape
     t0 = time.perf_counter()
-    oracle.run(wt, x)
+    oracle.run(wt, sample)
     dt = time.perf_counter() - t0
     return {"value": round(h * w / dt / 1e6, 5), "unit": "Mpx/s", "cores": oracle.threads(), "kind": "port",
-            "sample": f"one whole-image forward of a 1x3x{h}x{w} noisy image (BASELINE config 2 generator) "
-                      f"through oracle/scunet_oracle.cpp, the C++ restatement of src/cpu.rs; {dt:.2f} s",
+            "sample": f"the top {h} of the benchmark image's 1080 rows ({c}x{h}x{w}, {h * w / 1e6:.2f} Mpx) forwarded "
+                      f"as one image through oracle/scunet_oracle.cpp, the C++ restatement of src/cpu.rs, "
+                      f"on {oracle.threads()} threads; {dt:.2f} s",
             "seconds": round(dt, 3)}
 
 
@@ -122,7 +125,8 @@ def main():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-sample", type=int, nargs=2, default=(512, 512))
+    ap.add_argument("--cpu-rows", type=int, default=512,
+                    help="rows of the 1080p input the CPU baseline forwards (a multiple of 8)")
     ap.add_argument("--no-kernel-events", action="store_true",
                     help="time the steps without the per-launch event pairs")
     ap.add_argument("--no-attn-sweep", action="store_true", help="skip the config-5 attention sweep")
@@ -180,6 +184,28 @@ def main():
         raise RuntimeError("non-finite output")
     mpx = h * w / dt / 1e6
     log(f"bench: {dt * 1e3:.2f} ms/step, {mpx:.2f} Mpx/s")
+
+    # Per-step distribution: the same steps again, each synchronised on its own and without
+    # the per-launch events (min and median, as the reference's bench reports them).
+    per = []
+    for _ in range(args.steps):
+        t1 = time.perf_counter()
+        be.run_device(xp, c, h, w, yp)
+        be.synchronize()
+        per.append(time.perf_counter() - t1)
+    per.sort()
+    step_min, step_med = per[0], per[len(per) // 2]
+    log(f"bench: per-step (synchronised, no events) min {step_min * 1e3:.2f} ms, median {step_med * 1e3:.2f} ms")
+    # Host to host: backend::run on host buffers (H2D, pad, forward, crop, D2H). Reported
+    # beside the device-resident figure, never as it.
+    be.run_fused(x)
+    h2h = []
+    for _ in range(3):
+        t1 = time.perf_counter()
+        be.run_fused(x)
+        h2h.append(time.perf_counter() - t1)
+    h2h_med = sorted(h2h)[1]
+    log(f"bench: host to host (scunet_hip_run, PCIe included) {h2h_med * 1e3:.2f} ms, {h * w / h2h_med / 1e6:.2f} Mpx/s")
 
     # Rows are per (kernel class, UNet level "@Lk"); aggregate per class for the roofline.
     total_ms = max(sum(r[2] for r in rows), 1e-9)
@@ -242,8 +268,8 @@ def main():
 
     cpu = None
     if not args.no_cpu_baseline:
-        log(f"bench: CPU baseline (oracle) on {tuple(args.cpu_sample)} ...")
-        cpu = cpu_baseline(wpath, tuple(args.cpu_sample))
+        log(f"bench: CPU baseline (oracle) on the top {args.cpu_rows} rows of the input ...")
+        cpu = cpu_baseline(wpath, x, args.cpu_rows)
         log(f"bench: CPU baseline {cpu['value']} Mpx/s on {cpu['cores']} threads ({cpu['seconds']} s)")
 
     fp = be.footprint()
@@ -271,6 +297,10 @@ def main():
         "attention_sweep": sweep,
         "kernels": kernels,
         "cpu_baseline": cpu,
+        "step_ms": {"min": round(step_min * 1e3, 3), "median": round(step_med * 1e3, 3),
+                    "note": "per-step synchronised pass without per-launch events"},
+        "host_to_host": {"ms": round(h2h_med * 1e3, 3), "mpx_s": round(h * w / h2h_med / 1e6, 3),
+                         "note": "scunet_hip_run on host buffers: H2D + pad + forward + crop + D2H, median of 3"},
         "device_bytes": {"weights": fp[0], "scratch": fp[1]},
     }
     be.free(xp)
