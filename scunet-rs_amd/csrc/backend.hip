@@ -61,6 +61,7 @@ struct scunet_hip {
     bool prof = false;
     bool unfused_msa = false;            // route every level through the 3-launch attention half
     bool direct3x3 = false;              // the direct implicit-GEMM 3x3 instead of Winograd
+    bool wino16 = false;                 // Winograd with 16 output channels per unit only
     bool gemm1x1 = false;                // the tiled GEMM for every 1x1 (no resident weights, no chaining)
     bool separate_mlp = false;           // the MLP as its own kernel also at t = 32
     std::string tag;                     // appended to profiler class names ("@L0".."@L3")
@@ -246,6 +247,7 @@ bool run_conv3(scunet_hip* h, const std::string& name, Conv3Args c, bool relu) {
     const float* u = W(h, "@wino:" + name + ".weight");
     if (!h->direct3x3 && u && c.cin % 16 == 0 && c.cout % 16 == 0 && c.H % 2 == 0 && c.W % 2 == 0) {
         c.w = u;
+        c.cblock = h->wino16 ? 16 : 0;
         if (!conv3x3_winograd(c, relu, h->stream, &why)) return fail(h, why);
     } else {
         c.w = W(h, name + ".weight");
@@ -607,6 +609,7 @@ int scunet_hip_create(const char* path, scunet_hip** out) {
     h->unfused_msa = std::getenv("SCUNET_HIP_UNFUSED_MSA") != nullptr;
     // A/B switch: the direct implicit-GEMM 3x3 kernel instead of Winograd F(2x2,3x3).
     h->direct3x3 = std::getenv("SCUNET_HIP_DIRECT3X3") != nullptr;
+    h->wino16 = std::getenv("SCUNET_HIP_WINO16") != nullptr;
     h->gemm1x1 = std::getenv("SCUNET_HIP_GEMM1X1") != nullptr;
     h->separate_mlp = std::getenv("SCUNET_HIP_SEPARATE_MLP") != nullptr;
     if (!upload_weights(h.get())) {

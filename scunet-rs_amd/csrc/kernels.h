@@ -100,6 +100,7 @@ struct Conv3Args {
     float* out = nullptr;
     long ldo = 0;
     int H = 0, W = 0, cin = 0, cout = 0;
+    int cblock = 0;                // Winograd: output channels per unit (0 = 32 when possible, 16)
 };
 // relu=true: out = relu(conv); relu=false: out += conv (the conv half's residual).
 bool conv3x3(const Conv3Args& a, bool relu, hipStream_t s, const char** why);

@@ -11,6 +11,8 @@
 // as A and B agree on it.
 #include "kernels.h"
 
+#include <type_traits>
+
 #include <algorithm>
 #include <cmath>
 #include <cstdint>
@@ -1010,12 +1012,12 @@ bool conv3x3(const Conv3Args& a, bool relu, hipStream_t s, const char** why) {
 struct WinoUnit {
     int y0, x0, co0;
 };
-DEVI WinoUnit wino_unit(long u, int tx, int nb, long tiles) {
+DEVI WinoUnit wino_unit(long u, int tx, int nb, long tiles, int cbw = 16) {
     // u = 8 j + xcd; within an XCD, consecutive j walk the cout blocks of one tile.
     const long xcd = u & 7, j = u >> 3;
     const long sp = (j / nb) * 8 + xcd;
     WinoUnit w;
-    w.co0 = int(j % nb) * 16;
+    w.co0 = int(j % nb) * cbw;
     w.y0 = sp < tiles ? int(sp / tx) * 16 : -1;
     w.x0 = int(sp % tx) * 16;
     return w;
@@ -1166,6 +1168,226 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     }
 }
 
+// Winograd F(2x2, 3x3) with 32 output channels per unit. 8 waves: wave pair p owns tile
+// rows 2p, 2p+1 (16 tiles, lane li = tile), and within the pair wave half hh owns rows
+// 2hh, 2hh+1 of the transformed 4x4 positions, for both 16-channel blocks. A wave thus
+// needs 3 of the patch's 4 rows and half of the input transform per slice, for twice the
+// output channels of k_wino: a quarter of the transform work and half of the halo loads per
+// product. The output transform is linear in the rows, so each wave forms the partial 2x2
+// outputs of its rows; the pair exchanges the partials of one channel block each through
+// LDS, and each wave finishes (ReLU or residual) and stores one block.
+// ---------------------------------------------------------------------------
+template <bool RELU>
+__global__ __launch_bounds__(512) void k_wino2(Conv3Args a, long tiles, long units) {
+    // Two LDS buffers (halo + U each): slice k + 1 is written into one while slice k is read
+    // from the other, so a slice costs one barrier. 18-pixel halo rows keep both buffers
+    // within the CU's LDS (the patch reads then meet 2-way bank conflicts).
+    constexpr int BK = 16, LDC = BK + 4, HW = 18, HP = 18, LDU = BK + 8, CB = 32, XP = 20;
+    constexpr int HV = (HW * HW * 4 + 511) / 512;   // halo float4 per thread
+    constexpr int UV = 16 * CB * 4 / 512;           // U float4 per thread
+    constexpr int HSZ = HW * HP * LDC, BSZ = HSZ + 16 * CB * LDU;
+    __shared__ float lds[2 * BSZ];
+    static_assert(8 * 64 * XP <= BSZ, "exchange must fit in one buffer");
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int li = lane & 15, lg = lane >> 4, pair = wave >> 1, hh = wave & 1;
+    const int tx = (a.W + 15) >> 4, nb = a.cout / CB, nch = a.cin / BK;
+    const int tr = 2 * pair + (li >> 3), tc = li & 7;
+
+    constexpr unsigned NOFF = 0xffffffffu;
+    unsigned uoff[UV];
+#pragma unroll
+    for (int i = 0; i < UV; ++i) {
+        const int f = tid + i * 512;
+        const int xi = f >> 7, rem = f & 127, co = rem >> 2, c4 = rem & 3;
+        uoff[i] = (unsigned(xi) * unsigned(a.cout) + unsigned(co)) * unsigned(a.cin) + unsigned(c4 * 4);
+    }
+    auto halo_offsets = [&](const WinoUnit& w, unsigned (&ho)[HV]) {
+#pragma unroll
+        for (int i = 0; i < HV; ++i) {
+            const int f = tid + i * 512;
+            const int px = f >> 2, c4 = f & 3;
+            const int gy = w.y0 - 1 + px / HW, gx = w.x0 - 1 + px % HW;
+            const bool ok = f < HW * HW * 4 && w.y0 >= 0 && gy >= 0 && gy < a.H && gx >= 0 && gx < a.W;
+            ho[i] = ok ? (unsigned(gy) * unsigned(a.W) + unsigned(gx)) * unsigned(a.ldi) + unsigned(c4 * 4) : NOFF;
+        }
+    };
+    f4 rh[HV], ru[UV];
+    auto load = [&](const unsigned (&ho)[HV], int co0, int ci0) {
+        const float* hb = a.in + ci0;
+#pragma unroll
+        for (int i = 0; i < HV; ++i) rh[i] = ho[i] != NOFF ? ld4(hb + ho[i]) : f4{0.f, 0.f, 0.f, 0.f};
+        const float* ub = a.w + long(co0) * a.cin + ci0;
+#pragma unroll
+        for (int i = 0; i < UV; ++i) ru[i] = ld4(ub + uoff[i]);
+    };
+    auto stash = [&](float* buf) {
+#pragma unroll
+        for (int i = 0; i < HV; ++i) {
+            const int f = tid + i * 512;
+            if (f < HW * HW * 4) {
+                const int px = f >> 2;
+                st4(&buf[((px / HW) * HP + px % HW) * LDC + (f & 3) * 4], rh[i]);
+            }
+        }
+        float* us = buf + HSZ;
+#pragma unroll
+        for (int i = 0; i < UV; ++i) {
+            const int f = tid + i * 512;
+            st4(&us[(f >> 2) * LDU + (f & 3) * 4], ru[i]);
+        }
+    };
+    // acc[cb][ii][j]: M[2hh + ii][j] for channel block cb (co0 + 16 cb + 4lg .. +3).
+    f4 acc[2][2][4];
+    // One slice: the two rows of V = B^T d B this half owns, then 2 x 4 x 2 x 4 products.
+    auto slice = [&](auto HHc, const float* buf) {
+        constexpr int H2 = decltype(HHc)::value;
+        const float* Us = buf + HSZ;
+        f4 t[2][4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float* col = &buf[((2 * tr + H2) * HP + 2 * tc + j) * LDC + lg * 4];
+            const f4 da = ld4(col), db = ld4(col + HP * LDC), dc = ld4(col + 2 * HP * LDC);
+            if constexpr (H2 == 0) {         // rows d0, d1, d2: T0 = d0 - d2, T1 = d1 + d2
+                t[0][j] = da - dc;
+                t[1][j] = db + dc;
+            } else {                         // rows d1, d2, d3: T2 = d2 - d1, T3 = d1 - d3
+                t[0][j] = db - da;
+                t[1][j] = da - dc;
+            }
+        }
+#pragma unroll
+        for (int ii = 0; ii < 2; ++ii) {
+            const f4 v[4] = {t[ii][0] - t[ii][2], t[ii][1] + t[ii][2], t[ii][2] - t[ii][1], t[ii][1] - t[ii][3]};
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int cb = 0; cb < 2; ++cb) {
+                    const f4 uu = ld4(&Us[(((2 * H2 + ii) * 4 + j) * CB + cb * 16 + li) * LDU + lg * 4]);
+#pragma unroll
+                    for (int s4 = 0; s4 < 4; ++s4) acc[cb][ii][j] = mfma4(uu[s4], v[j][s4], acc[cb][ii][j]);
+                }
+        }
+    };
+
+    // Partial outputs of this half's rows: with r_i[0] = M[i][0] + M[i][1] + M[i][2] and
+    // r_i[1] = M[i][1] - M[i][2] - M[i][3], Y[0][b] = r_0 + r_1 + r_2 and
+    // Y[1][b] = r_1 - r_2 - r_3 (A^T = [1 1 1 0; 0 1 -1 -1]). This wave finishes channel
+    // block H2 and hands block 1 - H2 to its partner through LDS (the U buffer, free now).
+    auto finish = [&](auto HHc, const WinoUnit& w, float* Us, const f4 (&res)[2][2]) {
+        constexpr int H2 = decltype(HHc)::value;
+        f4 yp[2][2][2];
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb) {
+            f4 r[2][2];
+#pragma unroll
+            for (int ii = 0; ii < 2; ++ii) {
+                r[ii][0] = acc[cb][ii][0] + acc[cb][ii][1] + acc[cb][ii][2];
+                r[ii][1] = acc[cb][ii][1] - acc[cb][ii][2] - acc[cb][ii][3];
+            }
+#pragma unroll
+            for (int b = 0; b < 2; ++b) {
+                if constexpr (H2 == 0) {
+                    yp[cb][0][b] = r[0][b] + r[1][b];
+                    yp[cb][1][b] = r[1][b];
+                } else {
+                    yp[cb][0][b] = r[0][b];
+                    yp[cb][1][b] = f4{0.f, 0.f, 0.f, 0.f} - r[0][b] - r[1][b];
+                }
+            }
+        }
+        float* xo = &Us[((pair * 2 + (1 - H2)) * 64 + lane) * XP];
+#pragma unroll
+        for (int a0 = 0; a0 < 2; ++a0)
+#pragma unroll
+            for (int b = 0; b < 2; ++b) st4(xo + (a0 * 2 + b) * 4, yp[1 - H2][a0][b]);
+        __syncthreads();
+        if (w.y0 < 0) return;
+        const float* xi = &Us[((pair * 2 + H2) * 64 + lane) * XP];
+        const int co = w.co0 + H2 * 16 + lg * 4;
+#pragma unroll
+        for (int a0 = 0; a0 < 2; ++a0)
+#pragma unroll
+            for (int b = 0; b < 2; ++b) {
+                const int y = w.y0 + 2 * tr + a0, x = w.x0 + 2 * tc + b;
+                if (y >= a.H || x >= a.W) continue;
+                f4 v = yp[H2][a0][b] + ld4(xi + (a0 * 2 + b) * 4);
+                float* o = a.out + (long(y) * a.W + x) * a.ldo + co;
+                if constexpr (RELU) {
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) v[q] = fmaxf(v[q], 0.0f);
+                    st4(o, v);
+                } else {
+                    st4(o, res[a0][b] + v);
+                }
+            }
+    };
+    // The residual a unit's epilogue adds to (channel block hh of its 2x2 outputs), read at
+    // the start of the unit's last slice so that its latency is hidden by the products.
+    auto load_res = [&](const WinoUnit& w, f4 (&res)[2][2]) {
+#pragma unroll
+        for (int a0 = 0; a0 < 2; ++a0)
+#pragma unroll
+            for (int b = 0; b < 2; ++b) {
+                const int y = w.y0 + 2 * tr + a0, x = w.x0 + 2 * tc + b;
+                res[a0][b] = (w.y0 >= 0 && y < a.H && x < a.W)
+                                 ? ld4(a.out + (long(y) * a.W + x) * a.ldo + w.co0 + hh * 16 + lg * 4)
+                                 : f4{0.f, 0.f, 0.f, 0.f};
+            }
+    };
+
+    long u = blockIdx.x;
+    if (u >= units) return;
+    WinoUnit cur = wino_unit(u, tx, nb, tiles, CB);
+    unsigned hcur[HV], hnxt[HV];
+    halo_offsets(cur, hcur);
+    load(hcur, cur.co0, 0);
+    stash(lds);
+    __syncthreads();
+    int kb = 0;                              // buffer of the current slice
+    for (;;) {
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+            for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[cb][ii][j] = f4{0.f, 0.f, 0.f, 0.f};
+        const long un = u + gridDim.x;
+        const WinoUnit nxt = wino_unit(un, tx, nb, tiles, CB);
+        halo_offsets(nxt, hnxt);
+        f4 res[2][2];
+        for (int c = 0; c < nch; ++c) {
+            // Buffer kb holds slice c. The next step's slice is loaded now and stashed into
+            // the other buffer after this slice's products: that buffer was last read in the
+            // previous step, which every wave finished before the last barrier.
+            const bool more = c + 1 < nch || un < units;
+            if (c + 1 < nch) load(hcur, cur.co0, (c + 1) * BK);
+            else if (un < units) load(hnxt, nxt.co0, 0);
+            if constexpr (!RELU) {
+                if (c + 1 == nch) load_res(cur, res);
+            }
+            const float* buf = lds + kb * BSZ;
+            if (hh == 0) slice(std::integral_constant<int, 0>{}, buf);
+            else slice(std::integral_constant<int, 1>{}, buf);
+            if (more) stash(lds + (kb ^ 1) * BSZ);
+            __syncthreads();
+            kb ^= 1;
+        }
+        // The last slice's buffer (kb ^ 1) is free: every wave passed the barrier after
+        // reading it. The exchange goes there; a barrier after the reads keeps the next
+        // stash (into that buffer) from overwriting partials a wave has not read yet.
+        float* xbuf = lds + (kb ^ 1) * BSZ;
+        if (hh == 0) finish(std::integral_constant<int, 0>{}, cur, xbuf, res);
+        else finish(std::integral_constant<int, 1>{}, cur, xbuf, res);
+        __syncthreads();
+        if (un >= units) break;
+        u = un;
+        cur = nxt;
+#pragma unroll
+        for (int i = 0; i < HV; ++i) hcur[i] = hnxt[i];
+    }
+}
+
 bool conv3x3_winograd(const Conv3Args& a, bool relu, hipStream_t s, const char** why) {
     if (a.cin % 16 != 0 || a.cout % 16 != 0 || (a.H & 1) || (a.W & 1)) {
         *why = "conv3x3_winograd: cin and cout must be multiples of 16 and the plane even";
@@ -1175,28 +1397,41 @@ bool conv3x3_winograd(const Conv3Args& a, bool relu, hipStream_t s, const char**
         *why = "conv3x3_winograd: plane too large for 32-bit element offsets";
         return false;
     }
-    static int per_cu[2] = {-1, -1}, cus = 0;
-    int& pc = per_cu[relu ? 1 : 0];
+    const bool wide = a.cout % 32 == 0 && a.cin >= 32 && a.cblock != 16;
+    static int per_cu[4] = {-1, -1, -1, -1}, cus = 0;
+    int& pc = per_cu[(relu ? 1 : 0) + (wide ? 2 : 0)];
     if (pc < 0) {
         int dev = 0;
-        if (hipGetDevice(&dev) != hipSuccess ||
-            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-            hipOccupancyMaxActiveBlocksPerMultiprocessor(&pc, relu ? k_wino<true> : k_wino<false>, 256, 0) !=
-                hipSuccess) {
+        hipError_t e = hipGetDevice(&dev);
+        if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+        if (e == hipSuccess) {
+            if (wide)
+                e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&pc, relu ? k_wino2<true> : k_wino2<false>, 512, 0);
+            else
+                e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&pc, relu ? k_wino<true> : k_wino<false>, 256, 0);
+        }
+        if (e != hipSuccess) {
             *why = "conv3x3_winograd: device query failed";
             return false;
         }
         if (pc < 1) pc = 1;
     }
     const long tiles = long((a.W + 15) / 16) * ((a.H + 15) / 16);
-    const int nb = a.cout / 16;
+    const int nb = a.cout / (wide ? 32 : 16);
     // Units are numbered 8 j + xcd with j < ceil(tiles / 8) * nb; numbers whose tile is
     // past the end (the last partial group of 8) carry y0 = -1 and do no loads or stores.
     const long units = ((tiles + 7) / 8) * 8 * nb;
     const long grid = std::min<long>(units, long(cus) * pc);
-    dim3 g{unsigned(grid), 1u, 1u}, block{256u, 1u, 1u};
-    if (relu) hipLaunchKernelGGL(k_wino<true>, g, block, 0, s, a, tiles, units);
-    else hipLaunchKernelGGL(k_wino<false>, g, block, 0, s, a, tiles, units);
+    dim3 g{unsigned(grid), 1u, 1u};
+    if (wide) {
+        dim3 block{512u, 1u, 1u};
+        if (relu) hipLaunchKernelGGL(k_wino2<true>, g, block, 0, s, a, tiles, units);
+        else hipLaunchKernelGGL(k_wino2<false>, g, block, 0, s, a, tiles, units);
+    } else {
+        dim3 block{256u, 1u, 1u};
+        if (relu) hipLaunchKernelGGL(k_wino<true>, g, block, 0, s, a, tiles, units);
+        else hipLaunchKernelGGL(k_wino<false>, g, block, 0, s, a, tiles, units);
+    }
     return true;
 }
 

@@ -139,33 +139,41 @@ def test_1080p_properties(be):
     assert 0.0 < float(np.abs(a).mean()) < 10.0
 
 
-def test_direct_and_winograd_3x3_agree(weights_path, owt):
-    """The conv half's 3x3 convolutions by Winograd F(2x2,3x3) (the default) and by the
-    direct implicit GEMM: both against the oracle's cpu.rs conv3x3, op by op and in a block."""
-    from scunet_hip import Hip, synth
-    os.environ["SCUNET_HIP_DIRECT3X3"] = "1"
+def _hip_with(weights_path, env):
+    from scunet_hip import Hip
+    os.environ[env] = "1"
     try:
-        direct = Hip(weights_path)
+        return Hip(weights_path)
     finally:
-        del os.environ["SCUNET_HIP_DIRECT3X3"]
+        del os.environ[env]
+
+
+def test_direct_and_winograd_3x3_agree(weights_path, owt):
+    """The conv half's 3x3 convolutions by Winograd F(2x2,3x3) with 32 output channels per
+    unit (the default), with 16 (SCUNET_HIP_WINO16) and by the direct implicit GEMM
+    (SCUNET_HIP_DIRECT3X3): all against the oracle's cpu.rs conv3x3, op by op (planes that
+    end in partial 16x16 tiles included) and in a block."""
+    from scunet_hip import Hip, synth
+    direct = _hip_with(weights_path, "SCUNET_HIP_DIRECT3X3")
+    w16 = _hip_with(weights_path, "SCUNET_HIP_WINO16")
     wino = Hip(weights_path)
     try:
         for name, c, h, w in (("m_down1.0.conv_block.0", 32, 40, 24), ("m_down2.1.conv_block.2", 64, 16, 24),
-                              ("m_down3.2.conv_block.0", 128, 24, 16), ("m_body.0.conv_block.2", 256, 16, 16)):
+                              ("m_down3.2.conv_block.0", 128, 24, 16), ("m_body.0.conv_block.2", 256, 16, 16),
+                              ("m_up1.2.conv_block.0", 32, 18, 34), ("m_up2.3.conv_block.2", 64, 50, 6)):
             x = synth.seq(c * h * w, 0.37).reshape(c, h, w)
             want = O.conv3x3(x, owt.t[name + ".weight"])
-            a = wino.op_probe("conv3x3", name, x, c, c, h, w)
-            b = direct.op_probe("conv3x3", name, x, c, c, h, w)
-            close(f"winograd {name}", want, a, 1e-5)
-            close(f"direct {name}", want, b, 1e-5)
+            for tag, be in (("winograd", wino), ("winograd16", w16), ("direct", direct)):
+                close(f"{tag} {name} {h}x{w}", want, be.op_probe("conv3x3", name, x, c, c, h, w), 1e-5)
         for prefix, shift in (("m_down1.1", 4), ("m_body.2", 0)):
             c = sum(owt.block_dims(prefix))
             x = synth.seq(c * 24 * 32, 0.61).reshape(c, 24, 32)
             want = O.conv_trans_block(owt, prefix, x, shift)
-            assert max_abs(want, wino.block_dump(prefix, 24, 32, shift, x)) <= STAGE_TOL
-            assert max_abs(want, direct.block_dump(prefix, 24, 32, shift, x)) <= STAGE_TOL
+            for be in (wino, w16, direct):
+                assert max_abs(want, be.block_dump(prefix, 24, 32, shift, x)) <= STAGE_TOL
     finally:
         wino.close()
+        w16.close()
         direct.close()
 
 
