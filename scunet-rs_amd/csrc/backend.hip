@@ -62,11 +62,13 @@ struct scunet_hip {
     bool unfused_msa = false;            // route every level through the 3-launch attention half
     bool direct3x3 = false;              // the direct implicit-GEMM 3x3 instead of Winograd
     bool wino16 = false;                 // Winograd with 16 output channels per unit only
+    bool gemm2 = false;                  // one tile per workgroup GEMM (no persistent walker)
     bool gemm1x1 = false;                // the tiled GEMM for every 1x1 (no resident weights, no chaining)
     bool separate_mlp = false;           // the MLP as its own kernel also at t = 32
     std::string tag;                     // appended to profiler class names ("@L0".."@L3")
     std::vector<ProfRec> recs;
     std::vector<hipEvent_t> ev_pool;
+    hipEvent_t chain = nullptr;          // the last profiled launch's end event (shared start)
     size_t ev_used = 0;
     std::vector<std::string> report_names;
 
@@ -120,7 +122,10 @@ float* buf(scunet_hip* h, const std::string& role, size_t floats) {
     return slot.first;
 }
 
-// Profiling (cuda.rs:263-273): an event pair per launch when on.
+// Profiling (cuda.rs:263-273): HIP events around every launch when on. Consecutive
+// launches share the event between them (one launch's end is the next one's start), which
+// halves the events in the stream; a launch's time then includes the dispatch gap before
+// it. The chain restarts at each forward.
 struct Span {
     scunet_hip* h;
     std::string name;
@@ -128,8 +133,12 @@ struct Span {
     hipEvent_t e0 = nullptr;
     Span(scunet_hip* hh, const char* n, double f, double b) : h(hh), name(std::string(n) + hh->tag), flop(f), bytes(b) {
         if (!h->prof) return;
-        e0 = next();
-        hipEventRecord(e0, h->stream);
+        if (h->chain) {
+            e0 = h->chain;
+        } else {
+            e0 = next();
+            hipEventRecord(e0, h->stream);
+        }
     }
     hipEvent_t next() {
         if (h->ev_used == h->ev_pool.size()) {
@@ -144,6 +153,7 @@ struct Span {
         hipEvent_t e1 = next();
         hipEventRecord(e1, h->stream);
         h->recs.push_back({name, e0, e1, flop, bytes});
+        h->chain = e1;
     }
 };
 
@@ -232,7 +242,9 @@ bool run_gemm(scunet_hip* h, const char* cls, const GemmArgs& g, GemmA a, GemmE 
                           double(g.M) * g.N * (e == E_RESID ? 2 : (e == E_DUAL ? 2 : 1)));
     Span sp(h, cls, gemm_flop(g.M, g.N, g.K), bytes);
     const char* why = nullptr;
-    if (!gemm(g, a, e, h->stream, &why)) return fail(h, std::string(cls) + ": " + why);
+    GemmArgs gg = g;
+    gg.persistent = h->gemm2 ? 0 : 1;
+    if (!gemm(gg, a, e, h->stream, &why)) return fail(h, std::string(cls) + ": " + why);
     return launched(h, cls);
 }
 
@@ -443,6 +455,7 @@ bool walk(scunet_hip* h, const float* x, int hh, int ww, int H, int Wd, float* y
         Ws[k] = Wd >> k;
         P[k] = long(Hs[k]) * Ws[k];
     }
+    h->chain = nullptr;
     float* cur[4];
     float* skip[4] = {nullptr, nullptr, nullptr, nullptr};
     for (int k = 0; k < 4; ++k) {
@@ -542,6 +555,7 @@ template <typename F>
 int guard(scunet_hip* h, F&& f) {
     if (!h) return -1;
     h->err.clear();
+    h->chain = nullptr;   // a profiled launch never shares an event across API calls
     try {
         return f() ? 0 : 1;
     } catch (const std::exception& e) {
@@ -610,6 +624,7 @@ int scunet_hip_create(const char* path, scunet_hip** out) {
     // A/B switch: the direct implicit-GEMM 3x3 kernel instead of Winograd F(2x2,3x3).
     h->direct3x3 = std::getenv("SCUNET_HIP_DIRECT3X3") != nullptr;
     h->wino16 = std::getenv("SCUNET_HIP_WINO16") != nullptr;
+    h->gemm2 = std::getenv("SCUNET_HIP_GEMM2") != nullptr;
     h->gemm1x1 = std::getenv("SCUNET_HIP_GEMM1X1") != nullptr;
     h->separate_mlp = std::getenv("SCUNET_HIP_SEPARATE_MLP") != nullptr;
     if (!upload_weights(h.get())) {
@@ -718,6 +733,7 @@ int scunet_hip_profile(scunet_hip* h, int on) {
         h->prof = on != 0;
         h->recs.clear();
         h->ev_used = 0;
+        h->chain = nullptr;
         return true;
     });
 }
@@ -752,6 +768,7 @@ int scunet_hip_profile_report(scunet_hip* h, const char** names, long* launches,
         if (n) *n = int(v.size());
         h->recs.clear();
         h->ev_used = 0;
+        h->chain = nullptr;
         return true;
     });
 }

@@ -47,6 +47,7 @@ struct GemmArgs {
     int in_w = 0;   // A_S2D: input plane width; E_D2S: input plane width
     int cin = 0;    // A_S2D
     int cout = 0;   // E_D2S
+    int persistent = 1;   // the persistent tile walker for non-LN operands (0: one tile per workgroup)
 };
 
 // Returns false (and a reason) if no tile configuration fits the shape.

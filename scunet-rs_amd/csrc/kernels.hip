@@ -422,6 +422,223 @@ __global__ __launch_bounds__(256) void k_gemm2(GemmArgs g) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// Persistent form of k_gemm2 for the row and patch (A_S2D) A operands: as
+// many workgroups as fit on the chip walk the output tiles with a grid stride. In the last
+// K slice of a tile the next tile's first A rows and weight slice are already loaded, and
+// a residual the epilogue adds is read at the start of that slice, so neither a tile's
+// start nor its epilogue waits on memory. One barrier per K slice (the weight slices are
+// double-buffered in LDS; the epilogue uses registers only). Tile t = 8 j + xcd: the
+// N-blocks of one M-tile are consecutive j on one XCD and share its L2.
+// ---------------------------------------------------------------------------
+template <int MT, int BN, int KC, int AM, int EP>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_gemm3(GemmArgs g, long tiles) {
+    constexpr int NT = BN / 16, KG = KC / 16, LDB = KC + 8;
+    constexpr int BV = BN * KC / 4 / 256;
+    static_assert(BN * KC / 4 % 256 == 0, "weight slice must split evenly over 256 threads");
+    // The residual is read ahead when its registers fit (up to 8 float4 per lane).
+    constexpr bool RPRE = EP == E_RESID && MT * NT <= 8;
+    __shared__ float Bs[2 * BN * LDB];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int li = lane & 15, lg = lane >> 4;
+    const int ntn = g.N / BN, nch = g.K / KC;
+    const long mtiles = (g.M + 64 * MT - 1) / (64 * MT);
+    const long G = gridDim.x;
+    // Rows of this wave in tile t (g.M when the tile is past the end: no loads, no stores).
+    auto decode = [&](long t, long& m0, int& n0) {
+        const long xcd = t & 7, j = t >> 3;
+        const long mt = (j / ntn) * 8 + xcd;
+        n0 = int(j % ntn) * BN;
+        m0 = mt < mtiles ? mt * 64 * MT + wave * 16 * MT : g.M;
+    };
+    auto a_get = [&](long row, int k) -> f4 {
+        if (row >= g.M) return f4{0.f, 0.f, 0.f, 0.f};
+        if constexpr (AM == A_ADD2) return ld4(g.A + row * g.lda + k) + ld4(g.A2 + row * g.lda + k);
+        if constexpr (AM == A_S2D) {
+            const int tap = k / g.cin, ci = k - tap * g.cin;
+            const int ow = g.in_w >> 1;
+            const long oy = row / ow, ox = row - oy * ow;
+            const long ip = (2 * oy + (tap >> 1)) * long(g.in_w) + 2 * ox + (tap & 1);
+            return ld4(g.A + ip * g.cin + ci);
+        }
+        return ld4(g.A + row * g.lda + k);
+    };
+    f4 bpre[BV];
+    auto bload = [&](int n0, int k0) {
+#pragma unroll
+        for (int i = 0; i < BV; ++i) {
+            const int f = tid + i * 256;
+            const int row = f / (KC / 4), c4 = f % (KC / 4);
+            bpre[i] = ld4(g.W + long(n0 + row) * g.K + k0 + c4 * 4);
+        }
+    };
+    auto bstore = [&](int b) {
+#pragma unroll
+        for (int i = 0; i < BV; ++i) {
+            const int f = tid + i * 256;
+            const int row = f / (KC / 4), c4 = f % (KC / 4);
+            st4(&Bs[b * BN * LDB + row * LDB + c4 * 4], bpre[i]);
+        }
+    };
+    f4 acur[MT][KG], anext[MT][KG];
+    auto aload = [&](long m0, int k0, f4 (&dst)[MT][KG]) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int kg = 0; kg < KG; ++kg) dst[mt][kg] = a_get(m0 + mt * 16 + li, k0 + kg * 16 + lg * 4);
+    };
+    f4 acc[MT][NT], res[MT][NT];
+
+    long t = blockIdx.x;
+    if (t >= tiles) return;
+    long m0;
+    int n0;
+    decode(t, m0, n0);
+    bload(n0, 0);
+    aload(m0, 0, acur);
+    bstore(0);
+    __syncthreads();
+    int kb = 0;
+    for (;;) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = f4{0.f, 0.f, 0.f, 0.f};
+        const long tn = t + G;
+        long m0n = g.M;
+        int n0n = 0;
+        if (tn < tiles) decode(tn, m0n, n0n);
+        for (int c = 0; c < nch; ++c) {
+            const bool last = c + 1 == nch;
+            const bool more = !last || tn < tiles;
+            if (!last) {
+                bload(n0, (c + 1) * KC);
+                aload(m0, (c + 1) * KC, anext);
+            } else if (tn < tiles) {
+                bload(n0n, 0);
+                aload(m0n, 0, anext);
+            }
+            if constexpr (RPRE) {
+                if (last) {
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt) {
+                        const long row = m0 + mt * 16 + li;
+#pragma unroll
+                        for (int nt = 0; nt < NT; ++nt)
+                            res[mt][nt] = row < g.M ? ld4(g.R + row * g.ldr + n0 + nt * 16 + lg * 4)
+                                                    : f4{0.f, 0.f, 0.f, 0.f};
+                    }
+                }
+            }
+            const float* B = Bs + kb * BN * LDB;
+#pragma unroll
+            for (int kg = 0; kg < KG; ++kg) {
+                f4 b[NT];
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt) b[nt] = ld4(B + (nt * 16 + li) * LDB + kg * 16 + lg * 4);
+#pragma unroll
+                for (int s4 = 0; s4 < 4; ++s4)
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                        for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = mfma4(b[nt][s4], acur[mt][kg][s4], acc[mt][nt]);
+            }
+            if (more) bstore(kb ^ 1);
+            __syncthreads();
+            kb ^= 1;
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int kg = 0; kg < KG; ++kg) acur[mt][kg] = anext[mt][kg];
+        }
+        // Epilogue: each lane holds 4 consecutive output columns of one row.
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+            const int col = n0 + nt * 16 + lg * 4;
+            const f4 bv = g.bias ? ld4(g.bias + col) : f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+                const long row = m0 + mt * 16 + li;
+                if (row >= g.M) continue;
+                f4 v = acc[mt][nt] + bv;
+                if constexpr (EP == E_STORE) {
+                    st4(g.C + row * g.ldc + col, v);
+                } else if constexpr (EP == E_DUAL) {
+                    st4(g.C + row * g.ldc + col, v);
+                    st4(g.C2 + row * g.ldc + col, v);
+                } else if constexpr (EP == E_GELU) {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) v[r] = gelu_as(v[r]);
+                    st4(g.C + row * g.ldc + col, v);
+                } else if constexpr (EP == E_RESID) {
+                    st4(g.C + row * g.ldc + col, (RPRE ? res[mt][nt] : ld4(g.R + row * g.ldr + col)) + v);
+                } else {
+                    const long ii = row / g.in_w, jj = row - ii * g.in_w;
+                    const int tap = col / g.cout, co = col - tap * g.cout;
+                    const long oy = 2 * ii + (tap >> 1), ox = 2 * jj + (tap & 1);
+                    st4(g.C + (oy * 2 * g.in_w + ox) * g.cout + co, v);
+                }
+            }
+        }
+        if (tn >= tiles) break;
+        t = tn;
+        m0 = m0n;
+        n0 = n0n;
+    }
+}
+
+template <int MT, int BN, int KC, int AM, int EP>
+static void launch_gemm3_k(const GemmArgs& g, hipStream_t s) {
+    static int per_cu = -1, cus = 0;
+    if (per_cu < 0) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_gemm3<MT, BN, KC, AM, EP>, 256, 0) != hipSuccess)
+            per_cu = 1;
+        if (per_cu < 1) per_cu = 1;
+        if (cus < 1) cus = 256;
+    }
+    const long mtiles = (g.M + 64 * MT - 1) / (64 * MT);
+    const long tiles = ((mtiles + 7) / 8) * 8 * (g.N / BN);
+    dim3 grid{unsigned(std::min<long>(tiles, long(cus) * per_cu)), 1u, 1u}, block{256u, 1u, 1u};
+    hipLaunchKernelGGL((k_gemm3<MT, BN, KC, AM, EP>), grid, block, 0, s, g, tiles);
+}
+
+template <int MT, int BN, int KC, int AM>
+static void launch_gemm3_e(const GemmArgs& g, GemmE e, hipStream_t s) {
+    switch (e) {
+        case E_STORE: launch_gemm3_k<MT, BN, KC, AM, E_STORE>(g, s); break;
+        case E_DUAL: launch_gemm3_k<MT, BN, KC, AM, E_DUAL>(g, s); break;
+        case E_GELU: launch_gemm3_k<MT, BN, KC, AM, E_GELU>(g, s); break;
+        case E_RESID: launch_gemm3_k<MT, BN, KC, AM, E_RESID>(g, s); break;
+        case E_D2S: launch_gemm3_k<MT, BN, KC, AM, E_D2S>(g, s); break;
+    }
+}
+
+template <int MT, int BN, int KC>
+static void launch_gemm3_a(const GemmArgs& g, GemmA a, GemmE e, hipStream_t s) {
+    switch (a) {
+        case A_ROWS: launch_gemm3_e<MT, BN, KC, A_ROWS>(g, e, s); break;
+        case A_S2D: launch_gemm3_e<MT, BN, KC, A_S2D>(g, e, s); break;
+        default: break;
+    }
+}
+
+static bool launch_gemm3(const GemmArgs& g, GemmA a, GemmE e, hipStream_t s) {
+    // The LayerNorm operand keeps its row in registers (k_gemm2); the skip-sum operand with
+    // the depth-to-space epilogue measured faster one tile per workgroup (k_gemm2).
+    if (a == A_LN || a == A_ADD2) return false;
+    if (g.N % 64 == 0 && g.N <= 128) launch_gemm3_a<2, 64, 32>(g, a, e, s);
+    else if (g.N % 128 == 0) launch_gemm3_a<2, 128, 32>(g, a, e, s);
+    else if (g.N % 96 == 0) launch_gemm3_a<2, 96, 32>(g, a, e, s);
+    else if (g.N % 64 == 0) launch_gemm3_a<4, 64, 32>(g, a, e, s);
+    else if (g.N % 32 == 0) launch_gemm3_a<4, 32, 32>(g, a, e, s);
+    else return false;
+    return true;
+}
+
 template <int MT, int BN, int KC, int AM, int KLN>
 static void launch_gemm2_e(const GemmArgs& g, GemmE e, hipStream_t s) {
     const long tiles = ((g.M + 64 * MT - 1) / (64 * MT)) * (g.N / BN);
@@ -505,6 +722,7 @@ bool gemm(const GemmArgs& g, GemmA a, GemmE e, hipStream_t s, const char** why) 
         *why = "gemm: depth-to-space needs cout % 16 == 0 and N == 4 cout";
         return false;
     }
+    if (g.persistent && launch_gemm3(g, a, e, s)) return true;
     if (launch_gemm2(g, a, e, s)) return true;
     if (g.N % 128 == 0) launch_gemm_a<128, 128, 64, 64>(g, a, e, s);
     else if (g.N % 96 == 0) launch_gemm_a<128, 96, 32, 96>(g, a, e, s);
@@ -711,6 +929,12 @@ __global__ __launch_bounds__(256) void k_mlp(MlpArgs a) {
         for (int kg = 0; kg < KG; ++kg)
             xa[mt][kg] = r < a.M ? ld4(a.x + r * a.ldx + kg * 16 + lg * 4) : f4{0.f, 0.f, 0.f, 0.f};
     }
+    // The raw rows stay in registers for the residual.
+    f4 xr[MT][KG];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int kg = 0; kg < KG; ++kg) xr[mt][kg] = xa[mt][kg];
     // LayerNorm, two-pass (cpu.rs:338-357).
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
@@ -823,8 +1047,7 @@ __global__ __launch_bounds__(256) void k_mlp(MlpArgs a) {
         for (int mt = 0; mt < MT; ++mt) {
             const long row = row0 + mt * 16 + li;
             if (row < a.M) {
-                float* o = a.x + row * a.ldx + nt * 16 + lg * 4;
-                st4(o, ld4(o) + (acc2[mt][nt] + bv));
+                st4(a.x + row * a.ldx + nt * 16 + lg * 4, xr[mt][nt] + (acc2[mt][nt] + bv));
             }
         }
     }

@@ -246,3 +246,37 @@ def test_mlp_inside_window_kernel_and_separate_mlp_agree(weights_path, owt, weig
         finally:
             fused.close()
             sep.close()
+
+
+def test_persistent_and_tiled_gemm_agree(weights_path, owt):
+    """The GEMM-shaped operators (2x2 stride-2 and transposed convs, 1x1 at 256 channels,
+    linears) through the persistent tile walker (the default) and through one tile per
+    workgroup (SCUNET_HIP_GEMM2): both against the oracle, on row counts that end in a
+    partial tile, and every stage of a forward."""
+    from scunet_hip import Hip, synth
+    tiled = _hip_with(weights_path, "SCUNET_HIP_GEMM2")
+    pers = Hip(weights_path)
+    try:
+        for be, tag in ((pers, "persistent"), (tiled, "tiled")):
+            for name, ci, h, w in (("m_down1.4", 64, 10, 22), ("m_down3.4", 256, 6, 14), ("m_down2.4", 128, 34, 18)):
+                x = synth.seq(ci * h * w, 0.33).reshape(ci, h, w)
+                close(f"{tag} conv2x2s2 {name}", O.conv2x2s2(x, owt.t[name + ".weight"]),
+                      be.op_probe("conv2x2s2", name, x, ci, 2 * ci, h, w), 1e-5)
+            for name, ci, h, w in (("m_up3.0", 512, 5, 7), ("m_up1.0", 128, 9, 13), ("m_up2.0", 256, 3, 31)):
+                x = synth.seq(ci * h * w, 0.35).reshape(ci, h, w)
+                close(f"{tag} conv_t2x2 {name}", O.conv_t2x2(x, owt.t[name + ".weight"]),
+                      be.op_probe("conv_t2x2", name, x, ci, ci // 2, h, w), 1e-5)
+            for name, c, h, w in (("m_down3.1.conv1_1", 256, 7, 19), ("m_body.2.conv1_2", 512, 5, 9)):
+                x = synth.seq(c * h * w, 0.29).reshape(c, h, w)
+                want = O.conv1x1(x, owt.t[name + ".weight"].reshape(c, c), owt.t[name + ".bias"])
+                close(f"{tag} conv1x1 {name}", want, be.op_probe("conv1x1", name, x, c, c, h, w), 1e-5)
+        x = synth.noisy_image(41, 3, 64, 128, 15)
+        _, want = O.forward_dump(owt, x)
+        for be in (pers, tiled):
+            got = {}
+            be.forward_dump(x, lambda n, v: got.__setitem__(n, v))
+            for name in want:
+                assert max_abs(want[name], got[name]) <= STAGE_TOL, name
+    finally:
+        pers.close()
+        tiled.close()
