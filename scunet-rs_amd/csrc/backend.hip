@@ -164,7 +164,7 @@ const float* W(scunet_hip* h, const std::string& name) {
 
 // Upload every tensor once (cuda.rs:466-472 uploads lazily; here all at create), in the
 // layout its kernel reads:
-//   3x3 conv_block weights [co][ci][3][3] -> [tap][co][ci]
+//   3x3 conv_block weights [co][ci][3][3] -> [tap][co][ci], and as Winograd filters [16][co][ci]
 //   down-conv m_downN.K.weight [co][ci][2][2] -> [co][tap*ci]        (tap = ky*2 + kx)
 //   up-conv   m_upN.0.weight  [ci][co][2][2] -> [tap*co + co'][ci]
 //   everything else as stored; rel-pos tables -> lane-ordered bias tables.
