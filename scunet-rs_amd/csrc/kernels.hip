@@ -2128,6 +2128,201 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(T == 32 ? 2
     }
 }
 
+// ---------------------------------------------------------------------------
+// The window-attention half at t = 128 and 256 (cpu.rs:791-799), one workgroup per window
+// and one wave per head (t / 32 waves):
+//   1. four waves LayerNorm the window's 64 token rows (read through the shifted index
+//      map) into LDS;
+//   2. each wave computes its head's q, k, v from the normalised rows (weights from L2,
+//      operand layouts as in k_msa), the attention, and parks its 64 x 32 output in LDS;
+//   3. after a barrier each wave computes 32 of the t projection outputs of all 64 tokens
+//      from the parked head outputs (out^T = Wp O^T), adds bias and residual and writes the
+//      rows back through the same index map.
+// The qkv rows and the attention output never reach HBM; the projection of all heads needs
+// no cross-wave accumulation in registers.
+// ---------------------------------------------------------------------------
+template <int T>
+__global__ __launch_bounds__(T * 2) void k_wmsa(MsaArgs a, long nw) {
+    constexpr int HEADS = T / 32, KG = T / 16, LDX = T + 8;
+    __shared__ float xs[64 * LDX];   // normalised tokens [token][channel]
+    __shared__ float os[64 * LDX];   // head outputs [token][head * 32 + dim]
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int li = lane & 15, lg = lane >> 4;
+    const long wi = blockIdx.x;
+    const int wh = int(wi / a.nww), ww = int(wi - long(wh) * a.nww);
+    auto rowof = [&](int t) -> long {
+        int y = wh * 8 + (t >> 3) + a.shift;
+        int x = ww * 8 + (t & 7) + a.shift;
+        if (y >= a.H) y -= a.H;
+        if (x >= a.W) x -= a.W;
+        return long(y) * a.W + x;
+    };
+
+    // 1. LN1 (cpu.rs:338-357) of tokens 16w .. 16w + 15 by wave w < 4.
+    if (wave < 4) {
+        const long row = rowof(wave * 16 + li);
+        f4 v[KG];
+#pragma unroll
+        for (int kg = 0; kg < KG; ++kg) v[kg] = ld4(a.x + row * a.ldx + kg * 16 + lg * 4);
+        float sm = 0.f;
+#pragma unroll
+        for (int kg = 0; kg < KG; ++kg) sm += (v[kg].x + v[kg].y) + (v[kg].z + v[kg].w);
+        sm += __shfl_xor(sm, 16);
+        sm += __shfl_xor(sm, 32);
+        const float mu = sm / float(T);
+        float q = 0.f;
+#pragma unroll
+        for (int kg = 0; kg < KG; ++kg) {
+            f4 d = v[kg] - mu;
+            q += (d.x * d.x + d.y * d.y) + (d.z * d.z + d.w * d.w);
+        }
+        q += __shfl_xor(q, 16);
+        q += __shfl_xor(q, 32);
+        const float rs = 1.0f / sqrtf(q / float(T) + 1e-5f);
+#pragma unroll
+        for (int kg = 0; kg < KG; ++kg) {
+            f4 gg = ld4(a.ln_g + kg * 16 + lg * 4), bb = ld4(a.ln_b + kg * 16 + lg * 4);
+            st4(xs + (wave * 16 + li) * LDX + kg * 16 + lg * 4, (v[kg] - mu) * rs * gg + bb);
+        }
+    }
+    __syncthreads();
+
+    // 2. Head h = wave.
+    const int h = wave;
+    {
+        f4 qf[4][2], kf[4][2], vf[4][2];
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+            for (int d = 0; d < 2; ++d) qf[mt][d] = kf[mt][d] = vf[mt][d] = f4{0.f, 0.f, 0.f, 0.f};
+        const float* wq = a.wqkv + long(h * 32) * T;
+        const float* wk = a.wqkv + long(T + h * 32) * T;
+        const float* wv = a.wqkv + long(2 * T + h * 32) * T;
+#pragma unroll 2
+        for (int kg = 0; kg < KG; ++kg) {
+            f4 xb[4];
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt) xb[mt] = ld4(xs + (mt * 16 + li) * LDX + kg * 16 + lg * 4);
+#pragma unroll
+            for (int d = 0; d < 2; ++d) {
+                const f4 fq = ld4(wq + (d * 16 + li) * T + kg * 16 + lg * 4);
+                const f4 fk = ld4(wk + (d * 16 + li) * T + kg * 16 + lg * 4);
+                const f4 fv = ld4(wv + (d * 16 + li) * T + kg * 16 + lg * 4);
+#pragma unroll
+                for (int s4 = 0; s4 < 4; ++s4)
+#pragma unroll
+                    for (int mt = 0; mt < 4; ++mt) {
+                        qf[mt][d] = mfma4(fq[s4], xb[mt][s4], qf[mt][d]);
+                        kf[mt][d] = mfma4(fk[s4], xb[mt][s4], kf[mt][d]);
+                        vf[mt][d] = mfma4(xb[mt][s4], fv[s4], vf[mt][d]);
+                    }
+            }
+        }
+        // qf/kf lanes hold dims 16d + 4lg .. +3 of token 16mt + li; vf lanes hold dim
+        // 16d + li of tokens 16mt + 4lg .. +3.
+#pragma unroll
+        for (int d = 0; d < 2; ++d) {
+            const f4 bq = ld4(a.bqkv + h * 32 + d * 16 + lg * 4);
+            const f4 bk = ld4(a.bqkv + T + h * 32 + d * 16 + lg * 4);
+            const float bv = a.bqkv[2 * T + h * 32 + d * 16 + li];
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt) {
+                qf[mt][d] += bq;
+                kf[mt][d] += bk;
+                vf[mt][d] += bv;
+            }
+        }
+        const bool row_edge = a.shift > 0 && wh == a.nwh - 1;
+        const bool col_edge = a.shift > 0 && ww == a.nww - 1;
+        const float SENT = -3.4028234663852886e38f / 4.0f;
+        const float* tab = a.tab + (long(h) * 64 + lane) * 64;
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) {
+            f4 S[4];
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt) S[mt] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int G = 0; G < 2; ++G)
+#pragma unroll
+                for (int s4 = 0; s4 < 4; ++s4)
+#pragma unroll
+                    for (int mt = 0; mt < 4; ++mt) S[mt] = mfma4(kf[mt][G][s4], qf[nt][G][s4], S[mt]);
+            const bool q_row_lo = nt < 2;
+            const bool q_col_lo = (li & 7) < 4;
+            const bool k_col_lo = (lg & 1) == 0;
+            float mx = -INFINITY;
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt) {
+                const f4 b = ld4(tab + nt * 16 + mt * 4);
+                const bool hit = (row_edge && (q_row_lo != (mt < 2))) || (col_edge && (q_col_lo != k_col_lo));
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    float v = S[mt][r] * a.scale + b[r];
+                    if (hit) v = SENT;
+                    S[mt][r] = v;
+                    mx = fmaxf(mx, v);
+                }
+            }
+            mx = fmaxf(mx, __shfl_xor(mx, 16));
+            mx = fmaxf(mx, __shfl_xor(mx, 32));
+            float sum = 0.0f;
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const float e = __expf(S[mt][r] - mx);
+                    S[mt][r] = e;
+                    sum += e;
+                }
+            sum += __shfl_xor(sum, 16);
+            sum += __shfl_xor(sum, 32);
+            const float inv = 1.0f / sum;
+            f4 O[2] = {f4{0.f, 0.f, 0.f, 0.f}, f4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+            for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const float p = S[kt][r] * inv;
+#pragma unroll
+                    for (int nd = 0; nd < 2; ++nd) O[nd] = mfma4(vf[kt][nd][r], p, O[nd]);
+                }
+            // Lanes hold dims 16nd + 4lg .. +3 of query 16nt + li.
+#pragma unroll
+            for (int nd = 0; nd < 2; ++nd) st4(os + (nt * 16 + li) * LDX + h * 32 + nd * 16 + lg * 4, O[nd]);
+        }
+    }
+    __syncthreads();
+
+    // 3. Projection columns c0 .. c0 + 31 of all tokens, bias and residual.
+    const int c0 = wave * 32;
+    f4 acc[4][2];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) acc[mt][0] = acc[mt][1] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll 4
+    for (int kg = 0; kg < KG; ++kg) {
+        f4 ob[4];
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) ob[mt] = ld4(os + (mt * 16 + li) * LDX + kg * 16 + lg * 4);
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) {
+            const f4 fw = ld4(a.wp + long(c0 + ct * 16 + li) * T + kg * 16 + lg * 4);
+#pragma unroll
+            for (int s4 = 0; s4 < 4; ++s4)
+#pragma unroll
+                for (int mt = 0; mt < 4; ++mt) acc[mt][ct] = mfma4(fw[s4], ob[mt][s4], acc[mt][ct]);
+        }
+    }
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+        const long row = rowof(mt * 16 + li);
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) {
+            float* o = a.x + row * a.ldx + c0 + ct * 16 + lg * 4;
+            st4(o, ld4(o) + (acc[mt][ct] + ld4(a.bp + c0 + ct * 16 + lg * 4)));
+        }
+    }
+}
+
 bool msa_fused(const MsaArgs& a, hipStream_t s, const char** why) {
     const long nw = long(a.nwh) * a.nww;
     if (nw == 0) return true;
@@ -2139,8 +2334,13 @@ bool msa_fused(const MsaArgs& a, hipStream_t s, const char** why) {
     if (a.t == 32 && a.w0) hipLaunchKernelGGL((k_msa<32, true>), grid, block, 0, s, a, nw);
     else if (a.t == 32) hipLaunchKernelGGL((k_msa<32, false>), grid, block, 0, s, a, nw);
     else if (a.t == 64) hipLaunchKernelGGL((k_msa<64, false>), grid, block, 0, s, a, nw);
+    else if (a.t == 128 || a.t == 256) {
+        dim3 wgrid{unsigned(nw), 1u, 1u}, wblock{unsigned(a.t * 2), 1u, 1u};
+        if (a.t == 128) hipLaunchKernelGGL(k_wmsa<128>, wgrid, wblock, 0, s, a, nw);
+        else hipLaunchKernelGGL(k_wmsa<256>, wgrid, wblock, 0, s, a, nw);
+    }
     else {
-        *why = "msa_fused: t must be 32 or 64";
+        *why = "msa_fused: t must be 32, 64, 128 or 256";
         return false;
     }
     return true;

@@ -46,8 +46,9 @@ def test_config2_512_whole_image_matches_cpu(be, owt):
 
 
 def test_fused_and_three_launch_attention_halves_agree(weights_path, owt):
-    """The fused per-window kernel (t = 32, 64) and the LN+qkv / attention / proj launches
-    compute the same block; both against the oracle."""
+    """The fused per-window kernels (one wave per window at t = 32, 64; one wave per head at
+    t = 128, 256) and the LN+qkv / attention / proj launches compute the same block; both
+    against the oracle, unshifted and shifted (edge windows included)."""
     from scunet_hip import Hip, synth
     os.environ["SCUNET_HIP_UNFUSED_MSA"] = "1"
     try:
@@ -56,7 +57,9 @@ def test_fused_and_three_launch_attention_halves_agree(weights_path, owt):
         del os.environ["SCUNET_HIP_UNFUSED_MSA"]
     fus = Hip(weights_path)
     try:
-        for prefix, h, w, shift in (("m_down1.1", 24, 40, 4), ("m_down2.2", 16, 32, 0), ("m_up2.2", 32, 16, 4)):
+        for prefix, h, w, shift in (("m_down1.1", 24, 40, 4), ("m_down2.2", 16, 32, 0), ("m_up2.2", 32, 16, 4),
+                                    ("m_down3.1", 24, 16, 4), ("m_up3.2", 16, 40, 0), ("m_body.1", 24, 24, 4),
+                                    ("m_body.0", 8, 16, 0)):
             c = sum(owt.block_dims(prefix))
             x = synth.seq(c * h * w, 0.59).reshape(c, h, w)
             a = fus.block_dump(prefix, h, w, shift, x)
