@@ -152,7 +152,7 @@ struct MsaArgs {
     int nwh = 0, nww = 0, H = 0, W = 0, shift = 0;
     float scale = 0.f;
 };
-// t = 32, 64 (one wave per window, all heads) or 128, 256 (one workgroup per window, one
+// t = 32 (one wave per window, all heads) or 64, 128, 256 (one workgroup per window, one
 // wave per head); false otherwise. The MLP option is available at t = 32.
 bool msa_fused(const MsaArgs& a, hipStream_t s, const char** why);
 // Host-side construction of the lane-ordered bias table from rp [heads][15][15].

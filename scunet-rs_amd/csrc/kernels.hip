@@ -46,15 +46,20 @@ DEVI long xcd_swizzle(long b, long nb) {
 
 // GELU with the Abramowitz & Stegun 7.1.26 erf the reference's CPU path uses
 // (cpu.rs:293-332), evaluated in fp32 (|erf error| < 1.5e-7 + fp32 rounding).
+// With x = v/sqrt(2), t = 1/(1 + p|x|) and q = 0.5 t poly(t) e^(-x^2) (so that
+// erf(|x|) = 1 - 2q), gelu(v) = 0.5 v (1 + erf(x)) is v - v q for v >= 0 and v q for v < 0,
+// i.e. max(v, 0) - |v| q in both cases. The 1/sqrt(2) is folded into p and into the
+// exponent's constant (e^(-v^2/2) = 2^(-v^2 log2(e)/2)), the 0.5 into the coefficients.
 DEVI float gelu_as(float v) {
-    float x = v * 0.70710678118654752440f;
+    const float av = fabsf(v);
     // v_rcp_f32 (1 ulp) instead of an IEEE division: t enters a polynomial whose own
     // approximation error is 1.5e-7, so a 1-ulp reciprocal changes nothing measurable.
-    float t = __builtin_amdgcn_rcpf(1.0f + 0.3275911f * fabsf(x));
-    float y = 1.0f - (((((1.061405429f * t - 1.453152027f) * t) + 1.421413741f) * t - 0.284496736f) * t +
-                      0.254829592f) * t * __expf(-x * x);
-    float e = x >= 0.0f ? y : -y;
-    return 0.5f * v * (1.0f + e);
+    const float t = __builtin_amdgcn_rcpf(fmaf(av, 0.3275911f * 0.70710678118654752440f, 1.0f));
+    const float p = ((((0.5f * 1.061405429f) * t - 0.5f * 1.453152027f) * t + 0.5f * 1.421413741f) * t -
+                     0.5f * 0.284496736f) * t + 0.5f * 0.254829592f;
+    const float e = __builtin_amdgcn_exp2f(v * (v * (-0.5f * 1.4426950408889634f)));
+    const float q = p * t * e;
+    return fmaf(-av, q, fmaxf(v, 0.0f));
 }
 
 // ---------------------------------------------------------------------------
@@ -2129,9 +2134,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(T == 32 ? 2
 }
 
 // ---------------------------------------------------------------------------
-// The window-attention half at t = 128 and 256 (cpu.rs:791-799), one workgroup per window
-// and one wave per head (t / 32 waves):
-//   1. four waves LayerNorm the window's 64 token rows (read through the shifted index
+// The window-attention half at t = 64, 128 and 256 (cpu.rs:791-799), one workgroup per
+// window and one wave per head (t / 32 waves):
+//   1. the waves LayerNorm the window's 64 token rows (read through the shifted index
 //      map) into LDS;
 //   2. each wave computes its head's q, k, v from the normalised rows (weights from L2,
 //      operand layouts as in k_msa), the attention, and parks its 64 x 32 output in LDS;
@@ -2158,9 +2163,9 @@ __global__ __launch_bounds__(T * 2) void k_wmsa(MsaArgs a, long nw) {
         return long(y) * a.W + x;
     };
 
-    // 1. LN1 (cpu.rs:338-357) of tokens 16w .. 16w + 15 by wave w < 4.
-    if (wave < 4) {
-        const long row = rowof(wave * 16 + li);
+    // 1. LN1 (cpu.rs:338-357) of token tiles 16m .. 16m + 15, m = wave, wave + HEADS, ...
+    for (int m = wave; m < 4; m += HEADS) {
+        const long row = rowof(m * 16 + li);
         f4 v[KG];
 #pragma unroll
         for (int kg = 0; kg < KG; ++kg) v[kg] = ld4(a.x + row * a.ldx + kg * 16 + lg * 4);
@@ -2182,7 +2187,7 @@ __global__ __launch_bounds__(T * 2) void k_wmsa(MsaArgs a, long nw) {
 #pragma unroll
         for (int kg = 0; kg < KG; ++kg) {
             f4 gg = ld4(a.ln_g + kg * 16 + lg * 4), bb = ld4(a.ln_b + kg * 16 + lg * 4);
-            st4(xs + (wave * 16 + li) * LDX + kg * 16 + lg * 4, (v[kg] - mu) * rs * gg + bb);
+            st4(xs + (m * 16 + li) * LDX + kg * 16 + lg * 4, (v[kg] - mu) * rs * gg + bb);
         }
     }
     __syncthreads();
@@ -2333,10 +2338,10 @@ bool msa_fused(const MsaArgs& a, hipStream_t s, const char** why) {
     }
     if (a.t == 32 && a.w0) hipLaunchKernelGGL((k_msa<32, true>), grid, block, 0, s, a, nw);
     else if (a.t == 32) hipLaunchKernelGGL((k_msa<32, false>), grid, block, 0, s, a, nw);
-    else if (a.t == 64) hipLaunchKernelGGL((k_msa<64, false>), grid, block, 0, s, a, nw);
-    else if (a.t == 128 || a.t == 256) {
+    else if (a.t == 64 || a.t == 128 || a.t == 256) {
         dim3 wgrid{unsigned(nw), 1u, 1u}, wblock{unsigned(a.t * 2), 1u, 1u};
-        if (a.t == 128) hipLaunchKernelGGL(k_wmsa<128>, wgrid, wblock, 0, s, a, nw);
+        if (a.t == 64) hipLaunchKernelGGL(k_wmsa<64>, wgrid, wblock, 0, s, a, nw);
+        else if (a.t == 128) hipLaunchKernelGGL(k_wmsa<128>, wgrid, wblock, 0, s, a, nw);
         else hipLaunchKernelGGL(k_wmsa<256>, wgrid, wblock, 0, s, a, nw);
     }
     else {
