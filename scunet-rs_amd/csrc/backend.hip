@@ -362,8 +362,8 @@ bool block(scunet_hip* h, const std::string& p, float* x, int H, int Wd, int shi
     // transformer half, tokens = pixels of y[:, t:2t].
     float* yt = s.y + t;
     const double mlp_flop = 16.0 * double(P) * t * t;
-    // At t = 32 the MLP runs inside the window kernel, on the window's tokens.
-    const bool mlp_in_msa = t == 32 && !h->unfused_msa && !h->separate_mlp;
+    // At t <= 64 the MLP runs inside the window kernel, on the window's tokens.
+    const bool mlp_in_msa = t <= 64 && !h->unfused_msa && !h->separate_mlp;
     if (t <= 256 && !h->unfused_msa) {
         MsaArgs m;
         m.x = yt; m.ldx = c; m.ln_g = W(h, tp + ".ln1.weight"); m.ln_b = W(h, tp + ".ln1.bias");

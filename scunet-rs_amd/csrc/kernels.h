@@ -153,7 +153,7 @@ struct MsaArgs {
     float scale = 0.f;
 };
 // t = 32 (one wave per window, all heads) or 64, 128, 256 (one workgroup per window, one
-// wave per head); false otherwise. The MLP option is available at t = 32.
+// wave per head); false otherwise. The MLP option is available at t = 32, 64.
 bool msa_fused(const MsaArgs& a, hipStream_t s, const char** why);
 // Host-side construction of the lane-ordered bias table from rp [heads][15][15].
 void build_bias_table(const float* rp, int heads, float* tab);

@@ -2144,10 +2144,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(T == 32 ? 2
 //      from the parked head outputs (out^T = Wp O^T), adds bias and residual and writes the
 //      rows back through the same index map.
 // The qkv rows and the attention output never reach HBM; the projection of all heads needs
-// no cross-wave accumulation in registers.
+// no cross-wave accumulation in registers. With the MLP option (t = 64) the rows after the
+// attention residual stay in LDS and 4. the MLP runs on whole token tiles (two per wave,
+// weights from L2) before the single write-back. (At t = 128 a wave would own one tile, a
+// weight load would feed a quarter as many products, and the separate MLP kernel, which
+// shares LDS-staged weights over 64 rows, measured faster.)
 // ---------------------------------------------------------------------------
-template <int T>
-__global__ __launch_bounds__(T * 2) void k_wmsa(MsaArgs a, long nw) {
+template <int T, bool MLP>
+__global__ __launch_bounds__(T * 2) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_wmsa(MsaArgs a, long nw) {
     constexpr int HEADS = T / 32, KG = T / 16, LDX = T + 8;
     __shared__ float xs[64 * LDX];   // normalised tokens [token][channel]
     __shared__ float os[64 * LDX];   // head outputs [token][head * 32 + dim]
@@ -2317,32 +2321,127 @@ __global__ __launch_bounds__(T * 2) void k_wmsa(MsaArgs a, long nw) {
                 for (int mt = 0; mt < 4; ++mt) acc[mt][ct] = mfma4(fw[s4], ob[mt][s4], acc[mt][ct]);
         }
     }
+    if constexpr (!MLP) {
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
-        const long row = rowof(mt * 16 + li);
+        for (int mt = 0; mt < 4; ++mt) {
+            const long row = rowof(mt * 16 + li);
 #pragma unroll
-        for (int ct = 0; ct < 2; ++ct) {
-            float* o = a.x + row * a.ldx + c0 + ct * 16 + lg * 4;
-            st4(o, ld4(o) + (acc[mt][ct] + ld4(a.bp + c0 + ct * 16 + lg * 4)));
+            for (int ct = 0; ct < 2; ++ct) {
+                float* o = a.x + row * a.ldx + c0 + ct * 16 + lg * 4;
+                st4(o, ld4(o) + (acc[mt][ct] + ld4(a.bp + c0 + ct * 16 + lg * 4)));
+            }
+        }
+        return;
+    } else {
+        // The block's rows after the attention residual go to LDS (xs is free: phase 2 is
+        // over), so that phase 4 sees whole rows.
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+            const long row = rowof(mt * 16 + li);
+#pragma unroll
+            for (int ct = 0; ct < 2; ++ct) {
+                const int col = c0 + ct * 16 + lg * 4;
+                st4(xs + (mt * 16 + li) * LDX + col,
+                    ld4(a.x + row * a.ldx + col) + (acc[mt][ct] + ld4(a.bp + col)));
+            }
+        }
+        __syncthreads();
+        // 4. The MLP (cpu.rs:800-860) on whole token tiles: wave w takes tiles w, w + HEADS,
+        // ... (MT of them); LN2 in registers, the hidden layer 32 units at a time, transposed
+        // (H^T = W0c Xn^T is directly the second product's operand), GELU, the residual.
+        constexpr int MT = 4 / HEADS, HID = 4 * T, HC = 32, HT = HC / 16;
+        f4 xr[MT][KG], xn[MT][KG];
+#pragma unroll
+        for (int i = 0; i < MT; ++i) {
+            const int m = wave + i * HEADS;
+#pragma unroll
+            for (int kg = 0; kg < KG; ++kg) xr[i][kg] = ld4(xs + (m * 16 + li) * LDX + kg * 16 + lg * 4);
+            float sm = 0.f;
+#pragma unroll
+            for (int kg = 0; kg < KG; ++kg) sm += (xr[i][kg].x + xr[i][kg].y) + (xr[i][kg].z + xr[i][kg].w);
+            sm += __shfl_xor(sm, 16);
+            sm += __shfl_xor(sm, 32);
+            const float mu = sm / float(T);
+            float q = 0.f;
+#pragma unroll
+            for (int kg = 0; kg < KG; ++kg) {
+                f4 d = xr[i][kg] - mu;
+                q += (d.x * d.x + d.y * d.y) + (d.z * d.z + d.w * d.w);
+            }
+            q += __shfl_xor(q, 16);
+            q += __shfl_xor(q, 32);
+            const float rs = 1.0f / sqrtf(q / float(T) + 1e-5f);
+#pragma unroll
+            for (int kg = 0; kg < KG; ++kg) {
+                f4 gg = ld4(a.ln2_g + kg * 16 + lg * 4), bb = ld4(a.ln2_b + kg * 16 + lg * 4);
+                xn[i][kg] = (xr[i][kg] - mu) * rs * gg + bb;
+            }
+        }
+        f4 acc2[MT][KG];
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+#pragma unroll
+            for (int nt = 0; nt < KG; ++nt) acc2[i][nt] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll 1
+        for (int ch = 0; ch < HID / HC; ++ch) {
+            f4 acc1[HT][MT];
+#pragma unroll
+            for (int ht = 0; ht < HT; ++ht)
+#pragma unroll
+                for (int i = 0; i < MT; ++i) acc1[ht][i] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int kg = 0; kg < KG; ++kg)
+#pragma unroll
+                for (int ht = 0; ht < HT; ++ht) {
+                    const f4 wv = ld4(a.w0 + long(ch * HC + ht * 16 + li) * T + kg * 16 + lg * 4);
+#pragma unroll
+                    for (int s4 = 0; s4 < 4; ++s4)
+#pragma unroll
+                        for (int i = 0; i < MT; ++i) acc1[ht][i] = mfma4(wv[s4], xn[i][kg][s4], acc1[ht][i]);
+                }
+#pragma unroll
+            for (int ht = 0; ht < HT; ++ht) {
+                const f4 bb = ld4(a.b0 + ch * HC + ht * 16 + lg * 4);
+#pragma unroll
+                for (int i = 0; i < MT; ++i)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) acc1[ht][i][r] = gelu_as(acc1[ht][i][r] + bb[r]);
+            }
+#pragma unroll
+            for (int ht = 0; ht < HT; ++ht)
+#pragma unroll
+                for (int nt = 0; nt < KG; ++nt) {
+                    const f4 wv = ld4(a.w2 + long(nt * 16 + li) * HID + ch * HC + ht * 16 + lg * 4);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+#pragma unroll
+                        for (int i = 0; i < MT; ++i) acc2[i][nt] = mfma4(wv[r], acc1[ht][i][r], acc2[i][nt]);
+                }
+        }
+#pragma unroll
+        for (int i = 0; i < MT; ++i) {
+            const long row = rowof((wave + i * HEADS) * 16 + li);
+#pragma unroll
+            for (int nt = 0; nt < KG; ++nt)
+                st4(a.x + row * a.ldx + nt * 16 + lg * 4, xr[i][nt] + (acc2[i][nt] + ld4(a.b2 + nt * 16 + lg * 4)));
         }
     }
-}
-
-bool msa_fused(const MsaArgs& a, hipStream_t s, const char** why) {
+}bool msa_fused(const MsaArgs& a, hipStream_t s, const char** why) {
     const long nw = long(a.nwh) * a.nww;
     if (nw == 0) return true;
     dim3 grid{unsigned((nw + 3) / 4), 1u, 1u}, block{256u, 1u, 1u};
-    if (a.w0 && a.t != 32) {
-        *why = "msa_fused: the fused MLP is available at t = 32 only";
+    if (a.w0 && a.t != 32 && a.t != 64) {
+        *why = "msa_fused: the fused MLP is available at t = 32, 64";
         return false;
     }
     if (a.t == 32 && a.w0) hipLaunchKernelGGL((k_msa<32, true>), grid, block, 0, s, a, nw);
     else if (a.t == 32) hipLaunchKernelGGL((k_msa<32, false>), grid, block, 0, s, a, nw);
     else if (a.t == 64 || a.t == 128 || a.t == 256) {
         dim3 wgrid{unsigned(nw), 1u, 1u}, wblock{unsigned(a.t * 2), 1u, 1u};
-        if (a.t == 64) hipLaunchKernelGGL(k_wmsa<64>, wgrid, wblock, 0, s, a, nw);
-        else if (a.t == 128) hipLaunchKernelGGL(k_wmsa<128>, wgrid, wblock, 0, s, a, nw);
-        else hipLaunchKernelGGL(k_wmsa<256>, wgrid, wblock, 0, s, a, nw);
+        if (a.t == 64 && a.w0) hipLaunchKernelGGL((k_wmsa<64, true>), wgrid, wblock, 0, s, a, nw);
+        else if (a.t == 64) hipLaunchKernelGGL((k_wmsa<64, false>), wgrid, wblock, 0, s, a, nw);
+        else if (a.t == 128) hipLaunchKernelGGL((k_wmsa<128, false>), wgrid, wblock, 0, s, a, nw);
+        else hipLaunchKernelGGL((k_wmsa<256, false>), wgrid, wblock, 0, s, a, nw);
     }
     else {
         *why = "msa_fused: t must be 32, 64, 128 or 256";

@@ -223,10 +223,10 @@ def test_resident_chained_1x1_and_tiled_gemm_agree(weights_path, owt):
 
 
 def test_mlp_inside_window_kernel_and_separate_mlp_agree(weights_path, owt, weights_path_affine):
-    """At t = 32 the MLP (LN2, mlp.0, GELU, mlp.2, residual; cpu.rs:800-860) runs inside the
-    window-attention kernel on each window's tokens (the default) or as its own kernel
-    (SCUNET_HIP_SEPARATE_MLP): both against the oracle's block, unshifted and shifted, on the
-    identity-LN checkpoint and on one with random LayerNorm affines."""
+    """At t = 32 and 64 the MLP (LN2, mlp.0, GELU, mlp.2, residual; cpu.rs:800-860) runs
+    inside the window-attention kernel on each window's tokens (the default) or as its own
+    kernel (SCUNET_HIP_SEPARATE_MLP): both against the oracle's block, unshifted and shifted,
+    on the identity-LN checkpoint and on one with random LayerNorm affines."""
     from scunet_hip import Hip, synth
     for wpath in (weights_path, weights_path_affine):
         ow = owt if wpath == weights_path else O.Weights.load(wpath)
@@ -238,7 +238,9 @@ def test_mlp_inside_window_kernel_and_separate_mlp_agree(weights_path, owt, weig
         fused = Hip(wpath)
         try:
             for prefix, shift, (h, w) in (("m_down1.0", 0, (24, 40)), ("m_down1.1", 4, (32, 24)),
-                                          ("m_up1.3", 0, (16, 16)), ("m_up1.4", 4, (40, 48))):
+                                          ("m_up1.3", 0, (16, 16)), ("m_up1.4", 4, (40, 48)),
+                                          ("m_down2.1", 4, (24, 32)), ("m_up2.2", 0, (16, 24)),
+                                          ("m_down3.3", 4, (16, 24)), ("m_up3.1", 0, (24, 16))):
                 c = sum(ow.block_dims(prefix))
                 x = synth.seq(c * h * w, 0.53).reshape(c, h, w)
                 want = O.conv_trans_block(ow, prefix, x, shift)
