@@ -1405,17 +1405,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 // outputs of its rows; the pair exchanges the partials of one channel block each through
 // LDS, and each wave finishes (ReLU or residual) and stores one block.
 // ---------------------------------------------------------------------------
-template <bool RELU>
+template <bool RELU, bool URES>
 __global__ __launch_bounds__(512) void k_wino2(Conv3Args a, long tiles, long units) {
     // Two LDS buffers (halo + U each): slice k + 1 is written into one while slice k is read
     // from the other, so a slice costs one barrier. 18-pixel halo rows keep both buffers
     // within the CU's LDS (the patch reads then meet 2-way bank conflicts).
+    // URES (cin = cout = 32): the whole U [16][32][32] is loaded into LDS once per workgroup
+    // (unpadded, 16-byte slots XOR-swizzled by the row so that the operand reads stay
+    // conflict-free), slices stage only the halo, and the exchange has its own area.
     constexpr int BK = 16, LDC = BK + 4, HW = 18, HP = 18, LDU = BK + 8, CB = 32, XP = 20;
     constexpr int HV = (HW * HW * 4 + 511) / 512;   // halo float4 per thread
-    constexpr int UV = 16 * CB * 4 / 512;           // U float4 per thread
-    constexpr int HSZ = HW * HP * LDC, BSZ = HSZ + 16 * CB * LDU;
-    __shared__ float lds[2 * BSZ];
-    static_assert(8 * 64 * XP <= BSZ, "exchange must fit in one buffer");
+    constexpr int UV = URES ? 0 : 16 * CB * 4 / 512;  // U float4 per thread and slice
+    constexpr int HSZ = HW * HP * LDC, BSZ = URES ? HSZ : HSZ + 16 * CB * LDU;
+    constexpr int USZ = URES ? 16 * CB * 32 : 0, XSZ = URES ? 8 * 64 * XP : 0;
+    __shared__ float lds[2 * BSZ + USZ + XSZ];
+    static_assert(URES || 8 * 64 * XP <= BSZ, "exchange must fit in one buffer");
+    float* const ures = lds + 2 * BSZ;
+    float* const xres = ures + USZ;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int li = lane & 15, lg = lane >> 4, pair = wave >> 1, hh = wave & 1;
@@ -1423,7 +1429,7 @@ __global__ __launch_bounds__(512) void k_wino2(Conv3Args a, long tiles, long uni
     const int tr = 2 * pair + (li >> 3), tc = li & 7;
 
     constexpr unsigned NOFF = 0xffffffffu;
-    unsigned uoff[UV];
+    unsigned uoff[UV > 0 ? UV : 1];
 #pragma unroll
     for (int i = 0; i < UV; ++i) {
         const int f = tid + i * 512;
@@ -1440,7 +1446,7 @@ __global__ __launch_bounds__(512) void k_wino2(Conv3Args a, long tiles, long uni
             ho[i] = ok ? (unsigned(gy) * unsigned(a.W) + unsigned(gx)) * unsigned(a.ldi) + unsigned(c4 * 4) : NOFF;
         }
     };
-    f4 rh[HV], ru[UV];
+    f4 rh[HV], ru[UV > 0 ? UV : 1];
     auto load = [&](const unsigned (&ho)[HV], int co0, int ci0) {
         const float* hb = a.in + ci0;
 #pragma unroll
@@ -1458,6 +1464,7 @@ __global__ __launch_bounds__(512) void k_wino2(Conv3Args a, long tiles, long uni
                 st4(&buf[((px / HW) * HP + px % HW) * LDC + (f & 3) * 4], rh[i]);
             }
         }
+        if constexpr (URES) return;
         float* us = buf + HSZ;
 #pragma unroll
         for (int i = 0; i < UV; ++i) {
@@ -1468,7 +1475,7 @@ __global__ __launch_bounds__(512) void k_wino2(Conv3Args a, long tiles, long uni
     // acc[cb][ii][j]: M[2hh + ii][j] for channel block cb (co0 + 16 cb + 4lg .. +3).
     f4 acc[2][2][4];
     // One slice: the two rows of V = B^T d B this half owns, then 2 x 4 x 2 x 4 products.
-    auto slice = [&](auto HHc, const float* buf) {
+    auto slice = [&](auto HHc, const float* buf, int ci0) {
         constexpr int H2 = decltype(HHc)::value;
         const float* Us = buf + HSZ;
         f4 t[2][4];
@@ -1491,7 +1498,12 @@ __global__ __launch_bounds__(512) void k_wino2(Conv3Args a, long tiles, long uni
             for (int j = 0; j < 4; ++j)
 #pragma unroll
                 for (int cb = 0; cb < 2; ++cb) {
-                    const f4 uu = ld4(&Us[(((2 * H2 + ii) * 4 + j) * CB + cb * 16 + li) * LDU + lg * 4]);
+                    const int ur = ((2 * H2 + ii) * 4 + j) * CB + cb * 16 + li;
+                    f4 uu;
+                    if constexpr (URES)
+                        uu = ld4(&ures[ur * 32 + 4 * (((ci0 >> 2) + lg) ^ (2 * ((ur >> 2) & 3)))]);
+                    else
+                        uu = ld4(&Us[ur * LDU + lg * 4]);
 #pragma unroll
                     for (int s4 = 0; s4 < 4; ++s4) acc[cb][ii][j] = mfma4(uu[s4], v[j][s4], acc[cb][ii][j]);
                 }
@@ -1566,6 +1578,14 @@ __global__ __launch_bounds__(512) void k_wino2(Conv3Args a, long tiles, long uni
 
     long u = blockIdx.x;
     if (u >= units) return;
+    if constexpr (URES) {
+        // U [16 xi][32 co][32 ci]: row r = xi * 32 + co, 16-byte slot c4 of the row stored at
+        // slot c4 ^ (2 ((r >> 2) & 3)).
+        for (int f = tid; f < 16 * 32 * 8; f += 512) {
+            const int r = f >> 3, c4 = f & 7;
+            st4(&ures[r * 32 + 4 * (c4 ^ (2 * ((r >> 2) & 3)))], ld4(a.w + long(r) * 32 + c4 * 4));
+        }
+    }
     WinoUnit cur = wino_unit(u, tx, nb, tiles, CB);
     unsigned hcur[HV], hnxt[HV];
     halo_offsets(cur, hcur);
@@ -1595,8 +1615,8 @@ __global__ __launch_bounds__(512) void k_wino2(Conv3Args a, long tiles, long uni
                 if (c + 1 == nch) load_res(cur, res);
             }
             const float* buf = lds + kb * BSZ;
-            if (hh == 0) slice(std::integral_constant<int, 0>{}, buf);
-            else slice(std::integral_constant<int, 1>{}, buf);
+            if (hh == 0) slice(std::integral_constant<int, 0>{}, buf, c * BK);
+            else slice(std::integral_constant<int, 1>{}, buf, c * BK);
             if (more) stash(lds + (kb ^ 1) * BSZ);
             __syncthreads();
             kb ^= 1;
@@ -1604,10 +1624,12 @@ __global__ __launch_bounds__(512) void k_wino2(Conv3Args a, long tiles, long uni
         // The last slice's buffer (kb ^ 1) is free: every wave passed the barrier after
         // reading it. The exchange goes there; a barrier after the reads keeps the next
         // stash (into that buffer) from overwriting partials a wave has not read yet.
-        float* xbuf = lds + (kb ^ 1) * BSZ;
+        float* xbuf = URES ? xres : lds + (kb ^ 1) * BSZ;
         if (hh == 0) finish(std::integral_constant<int, 0>{}, cur, xbuf, res);
         else finish(std::integral_constant<int, 1>{}, cur, xbuf, res);
-        __syncthreads();
+        // The next stash goes into the exchange buffer unless it has its own area; the
+        // partials are read before the next unit's exchange (several barriers later).
+        if constexpr (!URES) __syncthreads();
         if (un >= units) break;
         u = un;
         cur = nxt;
@@ -1626,15 +1648,20 @@ bool conv3x3_winograd(const Conv3Args& a, bool relu, hipStream_t s, const char**
         return false;
     }
     const bool wide = a.cout % 32 == 0 && a.cin >= 32 && a.cblock != 16;
-    static int per_cu[4] = {-1, -1, -1, -1}, cus = 0;
-    int& pc = per_cu[(relu ? 1 : 0) + (wide ? 2 : 0)];
+    const bool ures = wide && a.cin == 32 && a.cout == 32;
+    static int per_cu[6] = {-1, -1, -1, -1, -1, -1}, cus = 0;
+    int& pc = per_cu[(relu ? 1 : 0) + (ures ? 4 : wide ? 2 : 0)];
     if (pc < 0) {
         int dev = 0;
         hipError_t e = hipGetDevice(&dev);
         if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
         if (e == hipSuccess) {
-            if (wide)
-                e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&pc, relu ? k_wino2<true> : k_wino2<false>, 512, 0);
+            if (ures)
+                e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&pc, relu ? k_wino2<true, true> : k_wino2<false, true>,
+                                                                 512, 0);
+            else if (wide)
+                e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&pc, relu ? k_wino2<true, false> : k_wino2<false, false>,
+                                                                 512, 0);
             else
                 e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&pc, relu ? k_wino<true> : k_wino<false>, 256, 0);
         }
@@ -1651,10 +1678,14 @@ bool conv3x3_winograd(const Conv3Args& a, bool relu, hipStream_t s, const char**
     const long units = ((tiles + 7) / 8) * 8 * nb;
     const long grid = std::min<long>(units, long(cus) * pc);
     dim3 g{unsigned(grid), 1u, 1u};
-    if (wide) {
+    if (ures) {
         dim3 block{512u, 1u, 1u};
-        if (relu) hipLaunchKernelGGL(k_wino2<true>, g, block, 0, s, a, tiles, units);
-        else hipLaunchKernelGGL(k_wino2<false>, g, block, 0, s, a, tiles, units);
+        if (relu) hipLaunchKernelGGL((k_wino2<true, true>), g, block, 0, s, a, tiles, units);
+        else hipLaunchKernelGGL((k_wino2<false, true>), g, block, 0, s, a, tiles, units);
+    } else if (wide) {
+        dim3 block{512u, 1u, 1u};
+        if (relu) hipLaunchKernelGGL((k_wino2<true, false>), g, block, 0, s, a, tiles, units);
+        else hipLaunchKernelGGL((k_wino2<false, false>), g, block, 0, s, a, tiles, units);
     } else {
         dim3 block{256u, 1u, 1u};
         if (relu) hipLaunchKernelGGL(k_wino<true>, g, block, 0, s, a, tiles, units);
