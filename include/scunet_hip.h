@@ -53,6 +53,19 @@ const char* scunet_hip_name(const scunet_hip* h);
 int scunet_hip_arch(const scunet_hip* h, int* in_nc, int* dim, int* head_dim, int* window,
                     int* config);
 
+/* --- arithmetic mode (no counterpart in the reference, whose GPU path is fp32 only) ---
+ * SCUNET_HIP_FP32 (the default): every product in fp32, the reference's arithmetic.
+ * SCUNET_HIP_FP16: the matrix products take fp16 operands (round to nearest even) with fp32
+ * accumulation; planes, residuals, LayerNorm, softmax and GELU stay fp32. Faster, and
+ * within a stated looser tolerance of the fp32 result (max abs error and PSNR against
+ * the fp32 output are part of the test suite and the benchmark report).
+ * The mode applies to the handle's following calls. */
+#define SCUNET_HIP_FP32 0
+#define SCUNET_HIP_FP16 1
+int scunet_hip_set_precision(scunet_hip* h, int mode);
+/* The handle's mode, or -1 for a null handle. */
+int scunet_hip_precision(const scunet_hip* h);
+
 /* --- the forward (src/backend.rs:23-25 Backend::forward; src/cuda.rs:1606-1848) --- */
 
 /* x: the already replicate-padded plane [c][hp][wp] (hp, wp multiples of 64, c = in_nc);

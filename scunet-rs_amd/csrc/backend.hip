@@ -65,6 +65,11 @@ struct scunet_hip {
     bool gemm2 = false;                  // one tile per workgroup GEMM (no persistent walker)
     bool gemm1x1 = false;                // the tiled GEMM for every 1x1 (no resident weights, no chaining)
     bool separate_mlp = false;           // the MLP as its own kernel also at t = 32
+    int h16 = 0;                         // 1: fp16 MFMA operands, fp32 accumulation and planes
+    // The k-permuted fp16 weight copies (built when the fp16 mode is first selected).
+    half_t* h16blob = nullptr;
+    size_t h16bytes = 0;
+    std::map<std::string, const half_t*> hw;
     std::string tag;                     // appended to profiler class names ("@L0".."@L3")
     std::vector<ProfRec> recs;
     std::vector<hipEvent_t> ev_pool;
@@ -77,6 +82,7 @@ struct scunet_hip {
         for (auto& kv : arena)
             if (kv.second.first) hipFree(kv.second.first);
         if (wblob) hipFree(wblob);
+        if (h16blob) hipFree(h16blob);
         for (auto e : ev_pool) hipEventDestroy(e);
         if (stream) hipStreamDestroy(stream);
     }
@@ -162,6 +168,14 @@ const float* W(scunet_hip* h, const std::string& name) {
     return it == h->w.end() ? nullptr : it->second;
 }
 
+// The fp16 copy of weight `name` when the handle is in the fp16 mode, else null (which
+// selects a kernel's fp32 path).
+const half_t* W16(scunet_hip* h, const std::string& name) {
+    if (!h->h16) return nullptr;
+    auto it = h->hw.find(name);
+    return it == h->hw.end() ? nullptr : it->second;
+}
+
 // Upload every tensor once (cuda.rs:466-472 uploads lazily; here all at create), in the
 // layout its kernel reads:
 //   3x3 conv_block weights [co][ci][3][3] -> [tap][co][ci], and as Winograd filters [16][co][ci]
@@ -231,6 +245,52 @@ bool upload_weights(scunet_hip* h) {
         at += (e.second.size() * 4 + 255) / 256 * 256;
     }
     return true;
+}
+
+// The fp16 mode's weight copies: every matrix weight whose reduction width K is a multiple
+// of 32, as [rows][K] in the layout the fp32 kernels read (after the repacking above),
+// converted and k-permuted on the device.
+bool build_h16_weights(scunet_hip* h) {
+    if (h->h16blob) return true;
+    const Weights& wt = h->wt;
+    struct Item { const float* src; long rows; int K; std::string name; };
+    std::vector<Item> items;
+    for (auto& kv : wt.all()) {
+        const std::string& n = kv.first;
+        const Tensor& t = kv.second;
+        if (n.size() < 7 || n.compare(n.size() - 7, 7, ".weight") != 0) continue;
+        long rows = 0;
+        int K = 0;
+        if (t.shape.size() == 2) {
+            rows = long(t.shape[0]); K = int(t.shape[1]);                      // linear [out][in]
+        } else if (t.shape.size() == 4 && n.find(".conv_block.") != std::string::npos) {
+            rows = 9L * long(t.shape[0]); K = int(t.shape[1]);                 // [tap][co][ci]
+        } else if (t.shape.size() == 4 && t.shape[2] == 1 && t.shape[3] == 1) {
+            rows = long(t.shape[0]); K = int(t.shape[1]);                      // 1x1 [co][ci]
+        } else if (t.shape.size() == 4 && t.shape[2] == 2 && t.shape[3] == 2) {
+            const bool up = n.find("m_up") == 0 && n.find(".0.weight") != std::string::npos;
+            if (up) { rows = 4L * long(t.shape[1]); K = int(t.shape[0]); }    // [tap*co][ci]
+            else { rows = long(t.shape[0]); K = 4 * int(t.shape[1]); }         // [co][tap*ci]
+        }
+        if (rows <= 0 || K % 32 != 0 || long(rows) * K != long(t.numel)) continue;
+        const float* src = W(h, n);
+        if (!src) continue;
+        items.push_back({src, rows, K, n});
+    }
+    size_t total = 0;
+    for (auto& it : items) total += (size_t(it.rows) * it.K * 2 + 255) / 256 * 256;
+    void* p = nullptr;
+    if (!ck(h, hipMalloc(&p, std::max<size_t>(total, 256)), "fp16 weights: hipMalloc")) return false;
+    h->h16blob = static_cast<half_t*>(p);
+    h->h16bytes = total;
+    char* at = static_cast<char*>(p);
+    for (auto& it : items) {
+        h16_permute(it.src, reinterpret_cast<half_t*>(at), it.rows, it.K, h->stream);
+        if (!launched(h, "fp16 weights")) return false;
+        h->hw[it.name] = reinterpret_cast<const half_t*>(at);
+        at += (size_t(it.rows) * it.K * 2 + 255) / 256 * 256;
+    }
+    return ck(h, hipStreamSynchronize(h->stream), "fp16 weights");
 }
 
 // Algorithmic FLOP / bytes for the profiler (fp32, 2 FLOP per multiply-add; bytes =
@@ -321,7 +381,9 @@ bool run_pconv(scunet_hip* h, const PconvArgs& a, PconvMode mode) {
                                 c * c * (mode == PC_CHAIN ? 2 : 1));
     Span sp(h, mode == PC_CHAIN ? "conv1x1_chain" : "conv1x1", flop, bytes);
     const char* why = nullptr;
-    if (!pconv(a, mode, h->stream, &why)) return fail(h, why);
+    PconvArgs aa = a;
+    aa.h16 = h->h16;
+    if (!pconv(aa, mode, h->stream, &why)) return fail(h, why);
     return launched(h, "conv1x1");
 }
 
@@ -370,10 +432,12 @@ bool block(scunet_hip* h, const std::string& p, float* x, int H, int Wd, int shi
         m.wqkv = W(h, tp + ".msa.embedding_layer.weight"); m.bqkv = W(h, tp + ".msa.embedding_layer.bias");
         m.wp = W(h, tp + ".msa.linear.weight"); m.bp = W(h, tp + ".msa.linear.bias"); m.tab = h->tab[p];
         m.t = t; m.nwh = H / 8; m.nww = Wd / 8; m.H = H; m.W = Wd; m.shift = shift; m.scale = h->scale;
+        m.hqkv = W16(h, tp + ".msa.embedding_layer.weight"); m.hp = W16(h, tp + ".msa.linear.weight");
         if (mlp_in_msa) {
             m.ln2_g = W(h, tp + ".ln2.weight"); m.ln2_b = W(h, tp + ".ln2.bias");
             m.w0 = W(h, tp + ".mlp.0.weight"); m.b0 = W(h, tp + ".mlp.0.bias");
             m.w2 = W(h, tp + ".mlp.2.weight"); m.b2 = W(h, tp + ".mlp.2.bias");
+            m.h0 = W16(h, tp + ".mlp.0.weight"); m.h2 = W16(h, tp + ".mlp.2.weight");
         }
         const double nw = double(m.nwh) * m.nww;
         const double msa_flop = 64.0 * nw * (8.0 * t * t) + 16384.0 * t * nw;
@@ -390,6 +454,7 @@ bool block(scunet_hip* h, const std::string& p, float* x, int H, int Wd, int shi
         m.x = yt; m.ldx = c; m.ln_g = W(h, tp + ".ln2.weight"); m.ln_b = W(h, tp + ".ln2.bias");
         m.w0 = W(h, tp + ".mlp.0.weight"); m.b0 = W(h, tp + ".mlp.0.bias");
         m.w2 = W(h, tp + ".mlp.2.weight"); m.b2 = W(h, tp + ".mlp.2.bias"); m.M = P; m.t = t;
+        m.h0 = W16(h, tp + ".mlp.0.weight"); m.h2 = W16(h, tp + ".mlp.2.weight");
         Span sp(h, "mlp_fused", mlp_flop, 4.0 * (2.0 * P * t + 8.0 * t * t + 5.0 * t));
         const char* why = nullptr;
         if (!mlp(m, h->stream, &why)) return fail(h, why);
@@ -641,6 +706,19 @@ const char* scunet_hip_last_error(const scunet_hip* h) { return h ? h->err.c_str
 
 const char* scunet_hip_name(const scunet_hip*) { return "hip"; }
 
+int scunet_hip_set_precision(scunet_hip* h, int mode) {
+    if (!h) return 1;
+    if (mode != SCUNET_HIP_FP32 && mode != SCUNET_HIP_FP16) {
+        fail(h, "scunet_hip_set_precision: mode must be SCUNET_HIP_FP32 (0) or SCUNET_HIP_FP16 (1)");
+        return 1;
+    }
+    if (mode == SCUNET_HIP_FP16 && !build_h16_weights(h)) return 1;
+    h->h16 = mode;
+    return 0;
+}
+
+int scunet_hip_precision(const scunet_hip* h) { return h ? h->h16 : -1; }
+
 int scunet_hip_arch(const scunet_hip* h, int* in_nc, int* dim, int* head_dim, int* window, int* config) {
     if (!h) return -1;
     if (in_nc) *in_nc = h->wt.in_nc;
@@ -706,7 +784,7 @@ int scunet_hip_footprint(const scunet_hip* h, size_t* weight_bytes, size_t* scra
     if (!h) return -1;
     size_t s = 0;
     for (auto& kv : h->arena) s += kv.second.second;
-    if (weight_bytes) *weight_bytes = h->wbytes;
+    if (weight_bytes) *weight_bytes = h->wbytes + h->h16bytes;
     if (scratch_bytes) *scratch_bytes = s;
     return 0;
 }

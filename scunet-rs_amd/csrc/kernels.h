@@ -13,6 +13,15 @@
 
 namespace scunet {
 
+// The fp16-operand mode. Matrix weights are kept a second time as fp16, rows [rows][K]
+// (K a multiple of 32) with k permuted inside each block of 32: position 32b + 8g + j holds
+// k = 32b + 4g + j for j < 4 and k = 32b + 16 + 4g + (j - 4) for j >= 4 (g = 0..3). That is
+// the order in which the kernels' f16 products consume k (each lane packs the 4 consecutive
+// k of two adjacent 16-wide k groups), so a lane's 8 operand halves are one 16-byte load.
+// Non-null h* pointers in the argument structs below select a kernel's fp16 path.
+using half_t = _Float16;
+void h16_permute(const float* src, half_t* dst, long rows, int K, hipStream_t s);
+
 // A-operand loaders of the GEMM.
 enum GemmA {
     A_ROWS = 0,   // A[m][k] = A[m*lda + k]
@@ -72,6 +81,7 @@ struct PconvArgs {
     float* C2 = nullptr;
     long M = 0;
     int c = 0;
+    int h16 = 0;                   // fp16 MFMA operands (fp32 accumulation)
 };
 // False (and a reason) for channel counts without a resident-weight configuration.
 bool pconv_supported(int c);
@@ -89,6 +99,8 @@ struct MlpArgs {
     const float* b0 = nullptr;     // [4t]
     const float* w2 = nullptr;     // [t][4t]
     const float* b2 = nullptr;     // [t]
+    const half_t* h0 = nullptr;    // fp16 mode: W0, W2 k-permuted
+    const half_t* h2 = nullptr;
     long M = 0;
     int t = 0;
 };
@@ -148,6 +160,11 @@ struct MsaArgs {
     const float* b0 = nullptr;
     const float* w2 = nullptr;     // [t][4t]
     const float* b2 = nullptr;
+    // fp16 mode: the k-permuted weights (hqkv, hp always; h0, h2 with the MLP option).
+    const half_t* hqkv = nullptr;
+    const half_t* hp = nullptr;
+    const half_t* h0 = nullptr;
+    const half_t* h2 = nullptr;
     int t = 0;
     int nwh = 0, nww = 0, H = 0, W = 0, shift = 0;
     float scale = 0.f;

@@ -25,6 +25,22 @@ typedef float f4 __attribute__((ext_vector_type(4)));
 
 DEVI f4 mfma4(float a, float b, f4 c) { return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0); }
 
+// The 16-bit operand mode: v_mfma_f32_16x16x32_f16 (fp16 operands, fp32 accumulation),
+// lane l supplying A[l % 16][8 (l / 16) + j] and B[8 (l / 16) + j][l % 16], j = 0..7 (checked
+// on the device). The fp32 kernels hand each lane 4 consecutive k of a 16-wide k group
+// (k = 16 kg + 4 lg + s); one f16 product takes the lane's float4s of two adjacent groups
+// 2kk and 2kk + 1, i.e. k = 32 kk + {4 lg .. 4 lg + 3} u {16 + 4 lg .. 16 + 4 lg + 3}. Both
+// operands see the same permutation of k, so the sum is unchanged, and an accumulator
+// (4 consecutive output channels per lane) is already the next product's operand.
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+DEVI h8 pack8(f4 lo, f4 hi) {
+    return h8{(_Float16)lo.x, (_Float16)lo.y, (_Float16)lo.z, (_Float16)lo.w,
+              (_Float16)hi.x, (_Float16)hi.y, (_Float16)hi.z, (_Float16)hi.w};
+}
+DEVI f4 mfma16(h8 a, h8 b, f4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0); }
+DEVI h8 ldh8(const _Float16* p) { return *reinterpret_cast<const h8*>(p); }
+DEVI void sth8(_Float16* p, h8 v) { *reinterpret_cast<h8*>(p) = v; }
+
 DEVI f4 ld4(const float* p) { return *reinterpret_cast<const f4*>(p); }
 // LDS row pitches: a wave's 16-byte LDS reads are conflict-free when, within each 32-lane
 // half, the 16-byte slot indices are distinct mod 32. The MFMA operand reads here have
@@ -746,18 +762,33 @@ bool gemm(const GemmArgs& g, GemmA a, GemmE e, hipStream_t s, const char** why) 
 // M rows), which leaves each lane holding 4 consecutive output channels of one pixel:
 // a float4 store, and, when chaining, exactly the pixel operand of the next product.
 // ---------------------------------------------------------------------------
-template <int C, int MT, int NW, int MODE, bool RPRE>
+template <int C, int MT, int NW, int MODE, bool RPRE, bool H16>
 __global__ __launch_bounds__(NW * 64) void k_pconv(PconvArgs a) {
-    constexpr int NT = C / 16, KG = C / 16, LDW = C + 8;
+    constexpr int NT = C / 16, KG = C / 16;
+    // fp32 rows: pitch C + 8 floats; fp16 rows: pitch C + 16 halves. Either way the pitch
+    // is 2 mod 4 sixteen-byte slots, so the 16 rows x 2 slots a 32-lane half reads are
+    // distinct mod 32: conflict-free 128-bit reads.
+    constexpr int LDW = H16 ? C + 16 : C + 8;
     constexpr int NMAT = MODE == PC_CHAIN ? 2 : 1;
-    __shared__ float Ws[NMAT * C * LDW];
+    using WT = std::conditional_t<H16, _Float16, float>;
+    __shared__ __align__(16) WT Ws[NMAT * C * LDW];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int li = lane & 15, lg = lane >> 4;
 
-    for (int f = tid; f < NMAT * C * C / 4; f += NW * 64) {
-        const int m = f / (C * C / 4), r = (f / (C / 4)) % C, c4 = f % (C / 4);
-        const float* src = m ? a.W1 : a.W;
-        st4(&Ws[m * C * LDW + r * LDW + c4 * 4], ld4(src + long(r) * C + c4 * 4));
+    if constexpr (H16) {
+        // Halves in the order the f16 product reads them: slot q = 4 kk + lg of row r holds
+        // W[r][32 kk + 4 lg + 0..3] and W[r][32 kk + 16 + 4 lg + 0..3].
+        for (int f = tid; f < NMAT * C * C / 8; f += NW * 64) {
+            const int m = f / (C * C / 8), r = (f / (C / 8)) % C, q = f % (C / 8);
+            const float* src = (m ? a.W1 : a.W) + long(r) * C + 32 * (q >> 2) + 4 * (q & 3);
+            sth8(&Ws[m * C * LDW + r * LDW + q * 8], pack8(ld4(src), ld4(src + 16)));
+        }
+    } else {
+        for (int f = tid; f < NMAT * C * C / 4; f += NW * 64) {
+            const int m = f / (C * C / 4), r = (f / (C / 4)) % C, c4 = f % (C / 4);
+            const float* src = m ? a.W1 : a.W;
+            st4(&Ws[m * C * LDW + r * LDW + c4 * 4], ld4(src + long(r) * C + c4 * 4));
+        }
     }
     __syncthreads();
 
@@ -774,22 +805,37 @@ __global__ __launch_bounds__(NW * 64) void k_pconv(PconvArgs a) {
                 dst[mt][kg] = row < a.M ? ld4(a.A + row * C + kg * 16 + lg * 4) : f4{0.f, 0.f, 0.f, 0.f};
         }
     };
-    auto product = [&](const float* Wm, const f4 (&x)[MT][KG], f4 (&acc)[MT][NT]) {
+    auto product = [&](const WT* Wm, const f4 (&x)[MT][KG], f4 (&acc)[MT][NT]) {
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
             for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = f4{0.f, 0.f, 0.f, 0.f};
+        if constexpr (H16) {
 #pragma unroll
-        for (int kg = 0; kg < KG; ++kg) {
-            f4 w[NT];
+            for (int kk = 0; kk < KG / 2; ++kk) {
+                h8 w[NT];
 #pragma unroll
-            for (int nt = 0; nt < NT; ++nt) w[nt] = ld4(Wm + (nt * 16 + li) * LDW + kg * 16 + lg * 4);
+                for (int nt = 0; nt < NT; ++nt) w[nt] = ldh8(Wm + (nt * 16 + li) * LDW + kk * 32 + lg * 8);
 #pragma unroll
-            for (int s = 0; s < 4; ++s)
+                for (int mt = 0; mt < MT; ++mt) {
+                    const h8 xv = pack8(x[mt][2 * kk], x[mt][2 * kk + 1]);
 #pragma unroll
-                for (int mt = 0; mt < MT; ++mt)
+                    for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = mfma16(w[nt], xv, acc[mt][nt]);
+                }
+            }
+        } else {
 #pragma unroll
-                    for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = mfma4(w[nt][s], x[mt][kg][s], acc[mt][nt]);
+            for (int kg = 0; kg < KG; ++kg) {
+                f4 w[NT];
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt) w[nt] = ld4(Wm + (nt * 16 + li) * LDW + kg * 16 + lg * 4);
+#pragma unroll
+                for (int s = 0; s < 4; ++s)
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                        for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = mfma4(w[nt][s], x[mt][kg][s], acc[mt][nt]);
+            }
         }
     };
 
@@ -820,7 +866,7 @@ __global__ __launch_bounds__(NW * 64) void k_pconv(PconvArgs a) {
         // hoisting every LDS weight read out of the loop into registers.
         int wz = 0;
         asm volatile("" : "+v"(wz));
-        const float* Wg = Ws + wz;
+        const WT* Wg = Ws + wz;
         f4 acc[MT][NT];
         product(Wg, cur, acc);
 #pragma unroll
@@ -864,14 +910,14 @@ __global__ __launch_bounds__(NW * 64) void k_pconv(PconvArgs a) {
     }
 }
 
-template <int C, int MT, int NW, int MODE, bool RPRE>
+template <int C, int MT, int NW, int MODE, bool RPRE, bool H16 = false>
 static bool launch_pconv(const PconvArgs& a, hipStream_t s) {
     static int per_cu = -1, cus = 0;
     if (per_cu < 0) {
         int dev = 0;
         if (hipGetDevice(&dev) != hipSuccess) return false;
         if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return false;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_pconv<C, MT, NW, MODE, RPRE>, NW * 64, 0) !=
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_pconv<C, MT, NW, MODE, RPRE, H16>, NW * 64, 0) !=
             hipSuccess)
             return false;
         if (per_cu < 1) per_cu = 1;
@@ -879,7 +925,7 @@ static bool launch_pconv(const PconvArgs& a, hipStream_t s) {
     const long groups = (a.M + 16 * MT - 1) / (16 * MT);
     const long waves = std::min<long>(groups, long(cus) * per_cu * NW);
     dim3 grid{unsigned((waves + NW - 1) / NW), 1u, 1u}, block{unsigned(NW * 64), 1u, 1u};
-    hipLaunchKernelGGL((k_pconv<C, MT, NW, MODE, RPRE>), grid, block, 0, s, a);
+    hipLaunchKernelGGL((k_pconv<C, MT, NW, MODE, RPRE, H16>), grid, block, 0, s, a);
     return true;
 }
 
@@ -888,7 +934,15 @@ bool pconv_supported(int c) { return c == 64 || c == 128; }
 bool pconv(const PconvArgs& a, PconvMode mode, hipStream_t s, const char** why) {
     if (a.M <= 0) return true;
     bool ok = false;
-    if (a.c == 64) {
+    if (a.h16 && a.c == 64) {
+        if (mode == PC_STORE) ok = launch_pconv<64, 2, 4, PC_STORE, false, true>(a, s);
+        else if (mode == PC_RESID) ok = launch_pconv<64, 2, 4, PC_RESID, false, true>(a, s);
+        else ok = launch_pconv<64, 2, 4, PC_CHAIN, false, true>(a, s);
+    } else if (a.h16 && a.c == 128) {
+        if (mode == PC_STORE) ok = launch_pconv<128, 1, 4, PC_STORE, false, true>(a, s);
+        else if (mode == PC_RESID) ok = launch_pconv<128, 1, 4, PC_RESID, false, true>(a, s);
+        else ok = launch_pconv<128, 1, 8, PC_CHAIN, false, true>(a, s);
+    } else if (a.c == 64) {
         if (mode == PC_STORE) ok = launch_pconv<64, 2, 4, PC_STORE, false>(a, s);
         else if (mode == PC_RESID) ok = launch_pconv<64, 2, 4, PC_RESID, false>(a, s);
         else ok = launch_pconv<64, 2, 4, PC_CHAIN, false>(a, s);
@@ -912,15 +966,20 @@ bool pconv(const PconvArgs& a, PconvMode mode, hipStream_t s, const char** why) 
 // H[row li][4 consecutive hidden units]: exactly the A operand of the second product, so
 // the hidden never goes through LDS or HBM. W0/W2 slices are double-buffered in LDS.
 // ---------------------------------------------------------------------------
-template <int T, int MT, int HC>
+template <int T, int MT, int HC, bool H16>
 __global__ __launch_bounds__(256) void k_mlp(MlpArgs a) {
     constexpr int KG = T / 16, NT = T / 16, HT = HC / 16, NCH = 4 * T / HC;
-    constexpr int L0 = T + 8, L2 = HC + 8;
+    // Slice pitches: fp32 T + 8 / HC + 8 floats; fp16 T + 16 / HC + 16 halves (2 mod 4
+    // sixteen-byte slots either way: conflict-free 128-bit operand reads).
+    constexpr int L0 = H16 ? T + 16 : T + 8, L2 = H16 ? HC + 16 : HC + 8;
     constexpr int BUF = HC * L0 + T * L2;
-    constexpr int W0V = HC * T / 4;               // float4 in a W0 slice
-    constexpr int PV = (2 * W0V) / 256;           // float4 per thread per slice (W0 then W2)
+    constexpr int EV = H16 ? 8 : 4;               // elements per 16-byte chunk
+    constexpr int W0V = HC * T / EV;              // chunks in a W0 slice (and in a W2 slice)
+    constexpr int PV = (2 * W0V) / 256;           // chunks per thread per slice (W0 then W2)
     static_assert((2 * W0V) % 256 == 0 && W0V % 256 == 0, "slice must split evenly");
-    __shared__ float lds[2 * BUF];
+    static_assert(!H16 || HC % 32 == 0, "fp16 slices are whole 32-wide k blocks");
+    using ET = std::conditional_t<H16, _Float16, float>;
+    __shared__ __align__(16) ET lds[2 * BUF];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int li = lane & 15, lg = lane >> 4;
@@ -964,34 +1023,47 @@ __global__ __launch_bounds__(256) void k_mlp(MlpArgs a) {
             xa[mt][kg] = (xa[mt][kg] - mu) * rs * g + b;
         }
     }
+    // fp16 operands of the first product (k groups 2kk, 2kk + 1 packed).
+    h8 xh[H16 ? MT : 1][H16 ? KG / 2 : 1];
+    if constexpr (H16) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int kk = 0; kk < KG / 2; ++kk) xh[mt][kk] = pack8(xa[mt][2 * kk], xa[mt][2 * kk + 1]);
+    }
 
+    // Slice ch: W0 rows ch HC .. + HC - 1 (all T columns) and W2 columns ch HC .. + HC - 1
+    // (all T rows). In fp16 mode both come from the k-permuted copies, whose 32-wide k
+    // blocks are whole within a slice.
     f4 pre[PV];
     auto gload = [&](int ch) {
 #pragma unroll
         for (int i = 0; i < PV; ++i) {
             const int f = tid + i * 256;
             if (f < W0V) {
-                const int row = f / (T / 4), c4 = f % (T / 4);
-                pre[i] = ld4(a.w0 + long(ch * HC + row) * T + c4 * 4);
+                const int row = f / (T / EV), c = f % (T / EV);
+                pre[i] = H16 ? ld4(reinterpret_cast<const float*>(a.h0 + long(ch * HC + row) * T + c * 8))
+                             : ld4(a.w0 + long(ch * HC + row) * T + c * 4);
             } else {
                 const int f2 = f - W0V;
-                const int row = f2 / (HC / 4), c4 = f2 % (HC / 4);
-                pre[i] = ld4(a.w2 + long(row) * (4 * T) + ch * HC + c4 * 4);
+                const int row = f2 / (HC / EV), c = f2 % (HC / EV);
+                pre[i] = H16 ? ld4(reinterpret_cast<const float*>(a.h2 + long(row) * (4 * T) + ch * HC + c * 8))
+                             : ld4(a.w2 + long(row) * (4 * T) + ch * HC + c * 4);
             }
         }
     };
     auto lstore = [&](int b) {
-        float* base = lds + b * BUF;
+        ET* base = lds + b * BUF;
 #pragma unroll
         for (int i = 0; i < PV; ++i) {
             const int f = tid + i * 256;
             if (f < W0V) {
-                const int row = f / (T / 4), c4 = f % (T / 4);
-                st4(base + row * L0 + c4 * 4, pre[i]);
+                const int row = f / (T / EV), c = f % (T / EV);
+                st4(reinterpret_cast<float*>(base + row * L0 + c * EV), pre[i]);
             } else {
                 const int f2 = f - W0V;
-                const int row = f2 / (HC / 4), c4 = f2 % (HC / 4);
-                st4(base + HC * L0 + row * L2 + c4 * 4, pre[i]);
+                const int row = f2 / (HC / EV), c = f2 % (HC / EV);
+                st4(reinterpret_cast<float*>(base + HC * L0 + row * L2 + c * EV), pre[i]);
             }
         }
     };
@@ -1006,23 +1078,34 @@ __global__ __launch_bounds__(256) void k_mlp(MlpArgs a) {
     lstore(0);
     __syncthreads();
     for (int ch = 0; ch < NCH; ++ch) {
-        const float* cur = lds + (ch & 1) * BUF;
+        const ET* cur = lds + (ch & 1) * BUF;
         if (ch + 1 < NCH) gload(ch + 1);
         f4 acc1[HT][MT];
 #pragma unroll
         for (int ht = 0; ht < HT; ++ht)
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt) acc1[ht][mt] = f4{0.f, 0.f, 0.f, 0.f};
+        if constexpr (H16) {
 #pragma unroll
-        for (int kg = 0; kg < KG; ++kg)
+            for (int kk = 0; kk < KG / 2; ++kk)
 #pragma unroll
-            for (int ht = 0; ht < HT; ++ht) {
-                const f4 wv = ld4(cur + (ht * 16 + li) * L0 + kg * 16 + lg * 4);
+                for (int ht = 0; ht < HT; ++ht) {
+                    const h8 wv = ldh8(cur + (ht * 16 + li) * L0 + kk * 32 + lg * 8);
 #pragma unroll
-                for (int s = 0; s < 4; ++s)
+                    for (int mt = 0; mt < MT; ++mt) acc1[ht][mt] = mfma16(wv, xh[mt][kk], acc1[ht][mt]);
+                }
+        } else {
 #pragma unroll
-                    for (int mt = 0; mt < MT; ++mt) acc1[ht][mt] = mfma4(wv[s], xa[mt][kg][s], acc1[ht][mt]);
-            }
+            for (int kg = 0; kg < KG; ++kg)
+#pragma unroll
+                for (int ht = 0; ht < HT; ++ht) {
+                    const f4 wv = ld4(cur + (ht * 16 + li) * L0 + kg * 16 + lg * 4);
+#pragma unroll
+                    for (int s = 0; s < 4; ++s)
+#pragma unroll
+                        for (int mt = 0; mt < MT; ++mt) acc1[ht][mt] = mfma4(wv[s], xa[mt][kg][s], acc1[ht][mt]);
+                }
+        }
 #pragma unroll
         for (int ht = 0; ht < HT; ++ht) {
             const f4 bb = ld4(a.b0 + ch * HC + ht * 16 + lg * 4);
@@ -1031,16 +1114,30 @@ __global__ __launch_bounds__(256) void k_mlp(MlpArgs a) {
 #pragma unroll
                 for (int r = 0; r < 4; ++r) acc1[ht][mt][r] = gelu_as(acc1[ht][mt][r] + bb[r]);
         }
+        if constexpr (H16) {
 #pragma unroll
-        for (int ht = 0; ht < HT; ++ht)
+            for (int kb = 0; kb < HT / 2; ++kb)
 #pragma unroll
-            for (int nt = 0; nt < NT; ++nt) {
-                const f4 wv = ld4(cur + HC * L0 + (nt * 16 + li) * L2 + ht * 16 + lg * 4);
+                for (int mt = 0; mt < MT; ++mt) {
+                    const h8 hv = pack8(acc1[2 * kb][mt], acc1[2 * kb + 1][mt]);
 #pragma unroll
-                for (int r = 0; r < 4; ++r)
+                    for (int nt = 0; nt < NT; ++nt) {
+                        const h8 wv = ldh8(cur + HC * L0 + (nt * 16 + li) * L2 + kb * 32 + lg * 8);
+                        acc2[mt][nt] = mfma16(wv, hv, acc2[mt][nt]);
+                    }
+                }
+        } else {
 #pragma unroll
-                    for (int mt = 0; mt < MT; ++mt) acc2[mt][nt] = mfma4(wv[r], acc1[ht][mt][r], acc2[mt][nt]);
-            }
+            for (int ht = 0; ht < HT; ++ht)
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt) {
+                    const f4 wv = ld4(cur + HC * L0 + (nt * 16 + li) * L2 + ht * 16 + lg * 4);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+#pragma unroll
+                        for (int mt = 0; mt < MT; ++mt) acc2[mt][nt] = mfma4(wv[r], acc1[ht][mt][r], acc2[mt][nt]);
+                }
+        }
         if (ch + 1 < NCH) lstore((ch + 1) & 1);
         __syncthreads();
     }
@@ -1065,11 +1162,16 @@ bool mlp(const MlpArgs& a, hipStream_t s, const char** why) {
         dim3 block{256u, 1u, 1u};
         hipLaunchKernelGGL(kern, grid, block, 0, s, a);
     };
+    if (a.h0 && !a.h2) {
+        *why = "mlp: the fp16 path needs both k-permuted weights";
+        return false;
+    }
+    const bool h16 = a.h0 != nullptr;
     switch (a.t) {
-        case 32: go(k_mlp<32, 4, 64>, 256); break;
-        case 64: go(k_mlp<64, 2, 64>, 128); break;
-        case 128: go(k_mlp<128, 1, 32>, 64); break;
-        case 256: go(k_mlp<256, 1, 16>, 64); break;
+        case 32: h16 ? go(k_mlp<32, 4, 64, true>, 256) : go(k_mlp<32, 4, 64, false>, 256); break;
+        case 64: h16 ? go(k_mlp<64, 2, 64, true>, 128) : go(k_mlp<64, 2, 64, false>, 128); break;
+        case 128: h16 ? go(k_mlp<128, 1, 32, true>, 64) : go(k_mlp<128, 1, 32, false>, 64); break;
+        case 256: h16 ? go(k_mlp<256, 1, 32, true>, 64) : go(k_mlp<256, 1, 16, false>, 64); break;
         default: *why = "mlp: t must be 32, 64, 128 or 256"; return false;
     }
     return true;
@@ -1888,32 +1990,42 @@ bool attention(const AttnArgs& a, hipStream_t s, const char** why) {
 //   3. x += out + bias, written back through the same index map (a permutation, so each
 //      window owns its 64 rows).
 // ---------------------------------------------------------------------------
-template <int T, bool MLP>
+template <int T, bool MLP, bool H16>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(T == 32 ? 2 : 1, 2))) void k_msa(MsaArgs a, long nw) {
-    constexpr int HEADS = T / 32, KG = T / 16, OT = T / 16, LDX = T + 4;
+    constexpr int HEADS = T / 32, KG = T / 16, OT = T / 16;
+    // Normalised tokens per wave: fp32 rows of T + 4 floats, or fp16 rows of T + 16 halves
+    // in the k-permuted order of the f16 products.
+    constexpr int LDX = H16 ? T + 16 : T + 4;
     // MLP weights, resident for the whole workgroup: W0 [4T][T] and W2 [T][4T] with row
-    // pitches T + 8 and 4T + 8 (conflict-free operand reads).
-    constexpr int HID = 4 * T, P0 = T + 8, P2 = HID + 8;
+    // pitches T + 8 and 4T + 8 floats (fp16: T + 16 and 4T + 16 halves, k-permuted), both
+    // conflict-free for 128-bit operand reads.
+    constexpr int HID = 4 * T, P0 = H16 ? T + 16 : T + 8, P2 = H16 ? HID + 16 : HID + 8;
     constexpr int MLPF = MLP ? HID * P0 + T * P2 : 0;
-    __shared__ float xs[4 * 64 * LDX + MLPF];
+    using ET = std::conditional_t<H16, _Float16, float>;
+    __shared__ __align__(16) ET xs[4 * 64 * LDX + MLPF];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    float* const wm0 = xs + 4 * 64 * LDX;
-    float* const wm2 = wm0 + HID * P0;
+    ET* const wm0 = xs + 4 * 64 * LDX;
+    ET* const wm2 = wm0 + HID * P0;
     if constexpr (MLP) {
-        for (int f = threadIdx.x; f < HID * T / 4; f += 256) {
-            const int r = f / (T / 4), c4 = f % (T / 4);
-            st4(wm0 + r * P0 + c4 * 4, ld4(a.w0 + long(r) * T + c4 * 4));
+        constexpr int EV = H16 ? 8 : 4;   // elements per 16-byte chunk
+        const ET* g0 = H16 ? reinterpret_cast<const ET*>(a.h0) : reinterpret_cast<const ET*>(a.w0);
+        const ET* g2 = H16 ? reinterpret_cast<const ET*>(a.h2) : reinterpret_cast<const ET*>(a.w2);
+        for (int f = threadIdx.x; f < HID * T / EV; f += 256) {
+            const int r = f / (T / EV), c = f % (T / EV);
+            st4(reinterpret_cast<float*>(wm0 + r * P0 + c * EV),
+                ld4(reinterpret_cast<const float*>(g0 + long(r) * T + c * EV)));
         }
-        for (int f = threadIdx.x; f < T * HID / 4; f += 256) {
-            const int r = f / (HID / 4), c4 = f % (HID / 4);
-            st4(wm2 + r * P2 + c4 * 4, ld4(a.w2 + long(r) * HID + c4 * 4));
+        for (int f = threadIdx.x; f < T * HID / EV; f += 256) {
+            const int r = f / (HID / EV), c = f % (HID / EV);
+            st4(reinterpret_cast<float*>(wm2 + r * P2 + c * EV),
+                ld4(reinterpret_cast<const float*>(g2 + long(r) * HID + c * EV)));
         }
     }
     const int li = lane & 15, lg = lane >> 4;
     const long wi = long(blockIdx.x) * 4 + wave;
     const bool valid = wi < nw;
     const int wh = valid ? int(wi / a.nww) : 0, ww = valid ? int(wi - long(wh) * a.nww) : 0;
-    float* xw = xs + wave * 64 * LDX;
+    ET* xw = xs + wave * 64 * LDX;
     auto rowof = [&](int t) -> long {
         int y = wh * 8 + (t >> 3) + a.shift;
         int x = ww * 8 + (t & 7) + a.shift;
@@ -1948,7 +2060,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(T == 32 ? 2
 #pragma unroll
             for (int kg = 0; kg < KG; ++kg) {
                 f4 gg = ld4(a.ln_g + kg * 16 + lg * 4), bb = ld4(a.ln_b + kg * 16 + lg * 4);
-                st4(xw + (mt * 16 + li) * LDX + kg * 16 + lg * 4, (v[kg] - mu) * rs * gg + bb);
+                v[kg] = (v[kg] - mu) * rs * gg + bb;
+            }
+            if constexpr (H16) {
+#pragma unroll
+                for (int kk = 0; kk < KG / 2; ++kk)
+                    sth8(xw + (mt * 16 + li) * LDX + kk * 32 + lg * 8, pack8(v[2 * kk], v[2 * kk + 1]));
+            } else {
+#pragma unroll
+                for (int kg = 0; kg < KG; ++kg) st4(xw + (mt * 16 + li) * LDX + kg * 16 + lg * 4, v[kg]);
             }
         }
     }
@@ -1971,27 +2091,51 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(T == 32 ? 2
         for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
             for (int d = 0; d < 2; ++d) qf[mt][d] = kf[mt][d] = vf[mt][d] = f4{0.f, 0.f, 0.f, 0.f};
-        const float* wq = a.wqkv + long(h * 32) * T;
-        const float* wk = a.wqkv + long(T + h * 32) * T;
-        const float* wv = a.wqkv + long(2 * T + h * 32) * T;
+        if constexpr (H16) {
+            const _Float16* wq = a.hqkv + long(h * 32) * T;
+            const _Float16* wk = a.hqkv + long(T + h * 32) * T;
+            const _Float16* wv = a.hqkv + long(2 * T + h * 32) * T;
 #pragma unroll
-        for (int kg = 0; kg < KG; ++kg) {
-            f4 xb[4];
+            for (int kk = 0; kk < KG / 2; ++kk) {
+                h8 xb[4];
 #pragma unroll
-            for (int mt = 0; mt < 4; ++mt) xb[mt] = ld4(xw + (mt * 16 + li) * LDX + kg * 16 + lg * 4);
+                for (int mt = 0; mt < 4; ++mt) xb[mt] = ldh8(xw + (mt * 16 + li) * LDX + kk * 32 + lg * 8);
 #pragma unroll
-            for (int d = 0; d < 2; ++d) {
-                const f4 fq = ld4(wq + (d * 16 + li) * T + kg * 16 + lg * 4);
-                const f4 fk = ld4(wk + (d * 16 + li) * T + kg * 16 + lg * 4);
-                const f4 fv = ld4(wv + (d * 16 + li) * T + kg * 16 + lg * 4);
-#pragma unroll
-                for (int s = 0; s < 4; ++s)
+                for (int d = 0; d < 2; ++d) {
+                    const h8 fq = ldh8(wq + (d * 16 + li) * T + kk * 32 + lg * 8);
+                    const h8 fk = ldh8(wk + (d * 16 + li) * T + kk * 32 + lg * 8);
+                    const h8 fv = ldh8(wv + (d * 16 + li) * T + kk * 32 + lg * 8);
 #pragma unroll
                     for (int mt = 0; mt < 4; ++mt) {
-                        qf[mt][d] = mfma4(fq[s], xb[mt][s], qf[mt][d]);
-                        kf[mt][d] = mfma4(fk[s], xb[mt][s], kf[mt][d]);
-                        vf[mt][d] = mfma4(xb[mt][s], fv[s], vf[mt][d]);
+                        qf[mt][d] = mfma16(fq, xb[mt], qf[mt][d]);
+                        kf[mt][d] = mfma16(fk, xb[mt], kf[mt][d]);
+                        vf[mt][d] = mfma16(xb[mt], fv, vf[mt][d]);
                     }
+                }
+            }
+        } else {
+            const float* wq = a.wqkv + long(h * 32) * T;
+            const float* wk = a.wqkv + long(T + h * 32) * T;
+            const float* wv = a.wqkv + long(2 * T + h * 32) * T;
+#pragma unroll
+            for (int kg = 0; kg < KG; ++kg) {
+                f4 xb[4];
+#pragma unroll
+                for (int mt = 0; mt < 4; ++mt) xb[mt] = ld4(xw + (mt * 16 + li) * LDX + kg * 16 + lg * 4);
+#pragma unroll
+                for (int d = 0; d < 2; ++d) {
+                    const f4 fq = ld4(wq + (d * 16 + li) * T + kg * 16 + lg * 4);
+                    const f4 fk = ld4(wk + (d * 16 + li) * T + kg * 16 + lg * 4);
+                    const f4 fv = ld4(wv + (d * 16 + li) * T + kg * 16 + lg * 4);
+#pragma unroll
+                    for (int s = 0; s < 4; ++s)
+#pragma unroll
+                        for (int mt = 0; mt < 4; ++mt) {
+                            qf[mt][d] = mfma4(fq[s], xb[mt][s], qf[mt][d]);
+                            kf[mt][d] = mfma4(fk[s], xb[mt][s], kf[mt][d]);
+                            vf[mt][d] = mfma4(xb[mt][s], fv[s], vf[mt][d]);
+                        }
+                }
             }
         }
         // Biases: qf/kf lanes hold dims 16d + 4lg .. +3 of token 16mt + li; vf lanes hold
@@ -2009,17 +2153,36 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(T == 32 ? 2
             }
         }
         const float* tab = a.tab + (long(h) * 64 + lane) * 64;
+        // fp16 operands of S^T = K Q^T (the head's 32 dims are one k block) and of
+        // O^T = V^T P^T (keys 32kk .. 32kk + 31 are k block kk).
+        h8 kh[H16 ? 4 : 1], qh[H16 ? 4 : 1], vh[H16 ? 2 : 1][2];
+        if constexpr (H16) {
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt) {
+                kh[mt] = pack8(kf[mt][0], kf[mt][1]);
+                qh[mt] = pack8(qf[mt][0], qf[mt][1]);
+            }
+#pragma unroll
+            for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+                for (int nd = 0; nd < 2; ++nd) vh[kk][nd] = pack8(vf[2 * kk][nd], vf[2 * kk + 1][nd]);
+        }
 #pragma unroll
         for (int nt = 0; nt < 4; ++nt) {
             f4 S[4];
 #pragma unroll
             for (int mt = 0; mt < 4; ++mt) S[mt] = f4{0.f, 0.f, 0.f, 0.f};
+            if constexpr (H16) {
 #pragma unroll
-            for (int G = 0; G < 2; ++G)
+                for (int mt = 0; mt < 4; ++mt) S[mt] = mfma16(kh[mt], qh[nt], S[mt]);
+            } else {
 #pragma unroll
-                for (int s = 0; s < 4; ++s)
+                for (int G = 0; G < 2; ++G)
 #pragma unroll
-                    for (int mt = 0; mt < 4; ++mt) S[mt] = mfma4(kf[mt][G][s], qf[nt][G][s], S[mt]);
+                    for (int s = 0; s < 4; ++s)
+#pragma unroll
+                        for (int mt = 0; mt < 4; ++mt) S[mt] = mfma4(kf[mt][G][s], qf[nt][G][s], S[mt]);
+            }
             const bool q_row_lo = nt < 2;
             const bool q_col_lo = (li & 7) < 4;
             const bool k_col_lo = (lg & 1) == 0;
@@ -2051,23 +2214,37 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(T == 32 ? 2
             sum += __shfl_xor(sum, 32);
             const float inv = 1.0f / sum;
             f4 O[2] = {f4{0.f, 0.f, 0.f, 0.f}, f4{0.f, 0.f, 0.f, 0.f}};
+            if constexpr (H16) {
 #pragma unroll
-            for (int kt = 0; kt < 4; ++kt)
+                for (int kk = 0; kk < 2; ++kk) {
+                    const h8 ph = pack8(S[2 * kk] * inv, S[2 * kk + 1] * inv);
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const float p = S[kt][r] * inv;
-#pragma unroll
-                    for (int nd = 0; nd < 2; ++nd) O[nd] = mfma4(vf[kt][nd][r], p, O[nd]);
+                    for (int nd = 0; nd < 2; ++nd) O[nd] = mfma16(vh[kk][nd], ph, O[nd]);
                 }
-            // out^T += Wp[:, head dims] O^T.
+                // out^T += Wp[:, head dims] O^T: the head's dims are k block h of Wp.
+                const h8 oh = pack8(O[0], O[1]);
 #pragma unroll
-            for (int ot = 0; ot < OT; ++ot)
+                for (int ot = 0; ot < OT; ++ot)
+                    acc[nt][ot] = mfma16(ldh8(a.hp + long(ot * 16 + li) * T + h * 32 + lg * 8), oh, acc[nt][ot]);
+            } else {
 #pragma unroll
-                for (int nd = 0; nd < 2; ++nd) {
-                    const f4 fw = ld4(a.wp + long(ot * 16 + li) * T + h * 32 + nd * 16 + lg * 4);
+                for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-                    for (int s = 0; s < 4; ++s) acc[nt][ot] = mfma4(fw[s], O[nd][s], acc[nt][ot]);
-                }
+                    for (int r = 0; r < 4; ++r) {
+                        const float p = S[kt][r] * inv;
+#pragma unroll
+                        for (int nd = 0; nd < 2; ++nd) O[nd] = mfma4(vf[kt][nd][r], p, O[nd]);
+                    }
+                // out^T += Wp[:, head dims] O^T.
+#pragma unroll
+                for (int ot = 0; ot < OT; ++ot)
+#pragma unroll
+                    for (int nd = 0; nd < 2; ++nd) {
+                        const f4 fw = ld4(a.wp + long(ot * 16 + li) * T + h * 32 + nd * 16 + lg * 4);
+#pragma unroll
+                        for (int s = 0; s < 4; ++s) acc[nt][ot] = mfma4(fw[s], O[nd][s], acc[nt][ot]);
+                    }
+            }
         }
     }
     // 3. Residual: lanes hold outputs 16ot + 4lg .. +3 of token 16nt + li.
@@ -2113,6 +2290,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(T == 32 ? 2
         for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
             for (int nt = 0; nt < OT; ++nt) acc2[mt][nt] = f4{0.f, 0.f, 0.f, 0.f};
+        h8 xnh[H16 ? 4 : 1][H16 ? OT / 2 : 1];
+        if constexpr (H16) {
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+                for (int kk = 0; kk < OT / 2; ++kk) xnh[mt][kk] = pack8(xn[mt][2 * kk], xn[mt][2 * kk + 1]);
+        }
 #pragma unroll 1
         for (int ch = 0; ch < HID / HC; ++ch) {
             f4 acc1[HT][4];
@@ -2120,16 +2304,27 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(T == 32 ? 2
             for (int ht = 0; ht < HT; ++ht)
 #pragma unroll
                 for (int mt = 0; mt < 4; ++mt) acc1[ht][mt] = f4{0.f, 0.f, 0.f, 0.f};
+            if constexpr (H16) {
 #pragma unroll
-            for (int kg = 0; kg < OT; ++kg)
+                for (int kk = 0; kk < OT / 2; ++kk)
 #pragma unroll
-                for (int ht = 0; ht < HT; ++ht) {
-                    const f4 wv = ld4(wm0 + (ch * HC + ht * 16 + li) * P0 + kg * 16 + lg * 4);
+                    for (int ht = 0; ht < HT; ++ht) {
+                        const h8 wv = ldh8(wm0 + (ch * HC + ht * 16 + li) * P0 + kk * 32 + lg * 8);
 #pragma unroll
-                    for (int s4 = 0; s4 < 4; ++s4)
+                        for (int mt = 0; mt < 4; ++mt) acc1[ht][mt] = mfma16(wv, xnh[mt][kk], acc1[ht][mt]);
+                    }
+            } else {
 #pragma unroll
-                        for (int mt = 0; mt < 4; ++mt) acc1[ht][mt] = mfma4(wv[s4], xn[mt][kg][s4], acc1[ht][mt]);
-                }
+                for (int kg = 0; kg < OT; ++kg)
+#pragma unroll
+                    for (int ht = 0; ht < HT; ++ht) {
+                        const f4 wv = ld4(wm0 + (ch * HC + ht * 16 + li) * P0 + kg * 16 + lg * 4);
+#pragma unroll
+                        for (int s4 = 0; s4 < 4; ++s4)
+#pragma unroll
+                            for (int mt = 0; mt < 4; ++mt) acc1[ht][mt] = mfma4(wv[s4], xn[mt][kg][s4], acc1[ht][mt]);
+                    }
+            }
 #pragma unroll
             for (int ht = 0; ht < HT; ++ht) {
                 const f4 bb = ld4(a.b0 + ch * HC + ht * 16 + lg * 4);
@@ -2138,16 +2333,27 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(T == 32 ? 2
 #pragma unroll
                     for (int r = 0; r < 4; ++r) acc1[ht][mt][r] = gelu_as(acc1[ht][mt][r] + bb[r]);
             }
+            if constexpr (H16) {
+                // HC = 32 hidden units: k block ch of W2.
 #pragma unroll
-            for (int ht = 0; ht < HT; ++ht)
+                for (int mt = 0; mt < 4; ++mt) {
+                    const h8 hv = pack8(acc1[0][mt], acc1[1][mt]);
 #pragma unroll
-                for (int nt = 0; nt < OT; ++nt) {
-                    const f4 wv = ld4(wm2 + (nt * 16 + li) * P2 + ch * HC + ht * 16 + lg * 4);
-#pragma unroll
-                    for (int r = 0; r < 4; ++r)
-#pragma unroll
-                        for (int mt = 0; mt < 4; ++mt) acc2[mt][nt] = mfma4(wv[r], acc1[ht][mt][r], acc2[mt][nt]);
+                    for (int nt = 0; nt < OT; ++nt)
+                        acc2[mt][nt] = mfma16(ldh8(wm2 + (nt * 16 + li) * P2 + ch * 32 + lg * 8), hv, acc2[mt][nt]);
                 }
+            } else {
+#pragma unroll
+                for (int ht = 0; ht < HT; ++ht)
+#pragma unroll
+                    for (int nt = 0; nt < OT; ++nt) {
+                        const f4 wv = ld4(wm2 + (nt * 16 + li) * P2 + ch * HC + ht * 16 + lg * 4);
+#pragma unroll
+                        for (int r = 0; r < 4; ++r)
+#pragma unroll
+                            for (int mt = 0; mt < 4; ++mt) acc2[mt][nt] = mfma4(wv[r], acc1[ht][mt][r], acc2[mt][nt]);
+                    }
+            }
         }
 #pragma unroll
         for (int nt = 0; nt < OT; ++nt) {
@@ -2181,11 +2387,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(T == 32 ? 2
 // weight load would feed a quarter as many products, and the separate MLP kernel, which
 // shares LDS-staged weights over 64 rows, measured faster.)
 // ---------------------------------------------------------------------------
-template <int T, bool MLP>
+template <int T, bool MLP, bool H16>
 __global__ __launch_bounds__(T * 2) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_wmsa(MsaArgs a, long nw) {
     constexpr int HEADS = T / 32, KG = T / 16, LDX = T + 8;
-    __shared__ float xs[64 * LDX];   // normalised tokens [token][channel]
-    __shared__ float os[64 * LDX];   // head outputs [token][head * 32 + dim]
+    // fp16 mode keeps the normalised tokens and the head outputs as k-permuted halves,
+    // rows of PH = T + 16 (conflict-free 128-bit reads), inside the same arrays.
+    constexpr int PH = T + 16;
+    static_assert(PH <= 2 * LDX, "fp16 rows fit the fp32 rows");
+    __shared__ __align__(16) float xs[64 * LDX];   // normalised tokens [token][channel]
+    __shared__ __align__(16) float os[64 * LDX];   // head outputs [token][head * 32 + dim]
+    _Float16* const xsh = reinterpret_cast<_Float16*>(xs);
+    _Float16* const osh = reinterpret_cast<_Float16*>(os);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int li = lane & 15, lg = lane >> 4;
     const long wi = blockIdx.x;
@@ -2222,7 +2434,15 @@ __global__ __launch_bounds__(T * 2) __attribute__((amdgpu_waves_per_eu(2, 2))) v
 #pragma unroll
         for (int kg = 0; kg < KG; ++kg) {
             f4 gg = ld4(a.ln_g + kg * 16 + lg * 4), bb = ld4(a.ln_b + kg * 16 + lg * 4);
-            st4(xs + (m * 16 + li) * LDX + kg * 16 + lg * 4, (v[kg] - mu) * rs * gg + bb);
+            v[kg] = (v[kg] - mu) * rs * gg + bb;
+        }
+        if constexpr (H16) {
+#pragma unroll
+            for (int kk = 0; kk < KG / 2; ++kk)
+                sth8(xsh + (m * 16 + li) * PH + kk * 32 + lg * 8, pack8(v[2 * kk], v[2 * kk + 1]));
+        } else {
+#pragma unroll
+            for (int kg = 0; kg < KG; ++kg) st4(xs + (m * 16 + li) * LDX + kg * 16 + lg * 4, v[kg]);
         }
     }
     __syncthreads();
@@ -2235,27 +2455,51 @@ __global__ __launch_bounds__(T * 2) __attribute__((amdgpu_waves_per_eu(2, 2))) v
         for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
             for (int d = 0; d < 2; ++d) qf[mt][d] = kf[mt][d] = vf[mt][d] = f4{0.f, 0.f, 0.f, 0.f};
-        const float* wq = a.wqkv + long(h * 32) * T;
-        const float* wk = a.wqkv + long(T + h * 32) * T;
-        const float* wv = a.wqkv + long(2 * T + h * 32) * T;
+        if constexpr (H16) {
+            const _Float16* wq = a.hqkv + long(h * 32) * T;
+            const _Float16* wk = a.hqkv + long(T + h * 32) * T;
+            const _Float16* wv = a.hqkv + long(2 * T + h * 32) * T;
 #pragma unroll 2
-        for (int kg = 0; kg < KG; ++kg) {
-            f4 xb[4];
+            for (int kk = 0; kk < KG / 2; ++kk) {
+                h8 xb[4];
 #pragma unroll
-            for (int mt = 0; mt < 4; ++mt) xb[mt] = ld4(xs + (mt * 16 + li) * LDX + kg * 16 + lg * 4);
+                for (int mt = 0; mt < 4; ++mt) xb[mt] = ldh8(xsh + (mt * 16 + li) * PH + kk * 32 + lg * 8);
 #pragma unroll
-            for (int d = 0; d < 2; ++d) {
-                const f4 fq = ld4(wq + (d * 16 + li) * T + kg * 16 + lg * 4);
-                const f4 fk = ld4(wk + (d * 16 + li) * T + kg * 16 + lg * 4);
-                const f4 fv = ld4(wv + (d * 16 + li) * T + kg * 16 + lg * 4);
-#pragma unroll
-                for (int s4 = 0; s4 < 4; ++s4)
+                for (int d = 0; d < 2; ++d) {
+                    const h8 fq = ldh8(wq + (d * 16 + li) * T + kk * 32 + lg * 8);
+                    const h8 fk = ldh8(wk + (d * 16 + li) * T + kk * 32 + lg * 8);
+                    const h8 fv = ldh8(wv + (d * 16 + li) * T + kk * 32 + lg * 8);
 #pragma unroll
                     for (int mt = 0; mt < 4; ++mt) {
-                        qf[mt][d] = mfma4(fq[s4], xb[mt][s4], qf[mt][d]);
-                        kf[mt][d] = mfma4(fk[s4], xb[mt][s4], kf[mt][d]);
-                        vf[mt][d] = mfma4(xb[mt][s4], fv[s4], vf[mt][d]);
+                        qf[mt][d] = mfma16(fq, xb[mt], qf[mt][d]);
+                        kf[mt][d] = mfma16(fk, xb[mt], kf[mt][d]);
+                        vf[mt][d] = mfma16(xb[mt], fv, vf[mt][d]);
                     }
+                }
+            }
+        } else {
+            const float* wq = a.wqkv + long(h * 32) * T;
+            const float* wk = a.wqkv + long(T + h * 32) * T;
+            const float* wv = a.wqkv + long(2 * T + h * 32) * T;
+#pragma unroll 2
+            for (int kg = 0; kg < KG; ++kg) {
+                f4 xb[4];
+#pragma unroll
+                for (int mt = 0; mt < 4; ++mt) xb[mt] = ld4(xs + (mt * 16 + li) * LDX + kg * 16 + lg * 4);
+#pragma unroll
+                for (int d = 0; d < 2; ++d) {
+                    const f4 fq = ld4(wq + (d * 16 + li) * T + kg * 16 + lg * 4);
+                    const f4 fk = ld4(wk + (d * 16 + li) * T + kg * 16 + lg * 4);
+                    const f4 fv = ld4(wv + (d * 16 + li) * T + kg * 16 + lg * 4);
+#pragma unroll
+                    for (int s4 = 0; s4 < 4; ++s4)
+#pragma unroll
+                        for (int mt = 0; mt < 4; ++mt) {
+                            qf[mt][d] = mfma4(fq[s4], xb[mt][s4], qf[mt][d]);
+                            kf[mt][d] = mfma4(fk[s4], xb[mt][s4], kf[mt][d]);
+                            vf[mt][d] = mfma4(xb[mt][s4], fv[s4], vf[mt][d]);
+                        }
+                }
             }
         }
         // qf/kf lanes hold dims 16d + 4lg .. +3 of token 16mt + li; vf lanes hold dim
@@ -2276,17 +2520,34 @@ __global__ __launch_bounds__(T * 2) __attribute__((amdgpu_waves_per_eu(2, 2))) v
         const bool col_edge = a.shift > 0 && ww == a.nww - 1;
         const float SENT = -3.4028234663852886e38f / 4.0f;
         const float* tab = a.tab + (long(h) * 64 + lane) * 64;
+        h8 kh[H16 ? 4 : 1], qh[H16 ? 4 : 1], vh[H16 ? 2 : 1][2];
+        if constexpr (H16) {
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt) {
+                kh[mt] = pack8(kf[mt][0], kf[mt][1]);
+                qh[mt] = pack8(qf[mt][0], qf[mt][1]);
+            }
+#pragma unroll
+            for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+                for (int nd = 0; nd < 2; ++nd) vh[kk][nd] = pack8(vf[2 * kk][nd], vf[2 * kk + 1][nd]);
+        }
 #pragma unroll
         for (int nt = 0; nt < 4; ++nt) {
             f4 S[4];
 #pragma unroll
             for (int mt = 0; mt < 4; ++mt) S[mt] = f4{0.f, 0.f, 0.f, 0.f};
+            if constexpr (H16) {
 #pragma unroll
-            for (int G = 0; G < 2; ++G)
+                for (int mt = 0; mt < 4; ++mt) S[mt] = mfma16(kh[mt], qh[nt], S[mt]);
+            } else {
 #pragma unroll
-                for (int s4 = 0; s4 < 4; ++s4)
+                for (int G = 0; G < 2; ++G)
 #pragma unroll
-                    for (int mt = 0; mt < 4; ++mt) S[mt] = mfma4(kf[mt][G][s4], qf[nt][G][s4], S[mt]);
+                    for (int s4 = 0; s4 < 4; ++s4)
+#pragma unroll
+                        for (int mt = 0; mt < 4; ++mt) S[mt] = mfma4(kf[mt][G][s4], qf[nt][G][s4], S[mt]);
+            }
             const bool q_row_lo = nt < 2;
             const bool q_col_lo = (li & 7) < 4;
             const bool k_col_lo = (lg & 1) == 0;
@@ -2318,17 +2579,28 @@ __global__ __launch_bounds__(T * 2) __attribute__((amdgpu_waves_per_eu(2, 2))) v
             sum += __shfl_xor(sum, 32);
             const float inv = 1.0f / sum;
             f4 O[2] = {f4{0.f, 0.f, 0.f, 0.f}, f4{0.f, 0.f, 0.f, 0.f}};
+            if constexpr (H16) {
 #pragma unroll
-            for (int kt = 0; kt < 4; ++kt)
+                for (int kk = 0; kk < 2; ++kk) {
+                    const h8 ph = pack8(S[2 * kk] * inv, S[2 * kk + 1] * inv);
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const float p = S[kt][r] * inv;
-#pragma unroll
-                    for (int nd = 0; nd < 2; ++nd) O[nd] = mfma4(vf[kt][nd][r], p, O[nd]);
+                    for (int nd = 0; nd < 2; ++nd) O[nd] = mfma16(vh[kk][nd], ph, O[nd]);
                 }
-            // Lanes hold dims 16nd + 4lg .. +3 of query 16nt + li.
+                // The head's dims are k block h of the projection.
+                sth8(osh + (nt * 16 + li) * PH + h * 32 + lg * 8, pack8(O[0], O[1]));
+            } else {
 #pragma unroll
-            for (int nd = 0; nd < 2; ++nd) st4(os + (nt * 16 + li) * LDX + h * 32 + nd * 16 + lg * 4, O[nd]);
+                for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const float p = S[kt][r] * inv;
+#pragma unroll
+                        for (int nd = 0; nd < 2; ++nd) O[nd] = mfma4(vf[kt][nd][r], p, O[nd]);
+                    }
+                // Lanes hold dims 16nd + 4lg .. +3 of query 16nt + li.
+#pragma unroll
+                for (int nd = 0; nd < 2; ++nd) st4(os + (nt * 16 + li) * LDX + h * 32 + nd * 16 + lg * 4, O[nd]);
+            }
         }
     }
     __syncthreads();
@@ -2338,18 +2610,33 @@ __global__ __launch_bounds__(T * 2) __attribute__((amdgpu_waves_per_eu(2, 2))) v
     f4 acc[4][2];
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) acc[mt][0] = acc[mt][1] = f4{0.f, 0.f, 0.f, 0.f};
+    if constexpr (H16) {
 #pragma unroll 4
-    for (int kg = 0; kg < KG; ++kg) {
-        f4 ob[4];
+        for (int kk = 0; kk < KG / 2; ++kk) {
+            h8 ob[4];
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt) ob[mt] = ld4(os + (mt * 16 + li) * LDX + kg * 16 + lg * 4);
+            for (int mt = 0; mt < 4; ++mt) ob[mt] = ldh8(osh + (mt * 16 + li) * PH + kk * 32 + lg * 8);
 #pragma unroll
-        for (int ct = 0; ct < 2; ++ct) {
-            const f4 fw = ld4(a.wp + long(c0 + ct * 16 + li) * T + kg * 16 + lg * 4);
+            for (int ct = 0; ct < 2; ++ct) {
+                const h8 fw = ldh8(a.hp + long(c0 + ct * 16 + li) * T + kk * 32 + lg * 8);
 #pragma unroll
-            for (int s4 = 0; s4 < 4; ++s4)
+                for (int mt = 0; mt < 4; ++mt) acc[mt][ct] = mfma16(fw, ob[mt], acc[mt][ct]);
+            }
+        }
+    } else {
+#pragma unroll 4
+        for (int kg = 0; kg < KG; ++kg) {
+            f4 ob[4];
 #pragma unroll
-                for (int mt = 0; mt < 4; ++mt) acc[mt][ct] = mfma4(fw[s4], ob[mt][s4], acc[mt][ct]);
+            for (int mt = 0; mt < 4; ++mt) ob[mt] = ld4(os + (mt * 16 + li) * LDX + kg * 16 + lg * 4);
+#pragma unroll
+            for (int ct = 0; ct < 2; ++ct) {
+                const f4 fw = ld4(a.wp + long(c0 + ct * 16 + li) * T + kg * 16 + lg * 4);
+#pragma unroll
+                for (int s4 = 0; s4 < 4; ++s4)
+#pragma unroll
+                    for (int mt = 0; mt < 4; ++mt) acc[mt][ct] = mfma4(fw[s4], ob[mt][s4], acc[mt][ct]);
+            }
         }
     }
     if constexpr (!MLP) {
@@ -2413,6 +2700,13 @@ __global__ __launch_bounds__(T * 2) __attribute__((amdgpu_waves_per_eu(2, 2))) v
         for (int i = 0; i < MT; ++i)
 #pragma unroll
             for (int nt = 0; nt < KG; ++nt) acc2[i][nt] = f4{0.f, 0.f, 0.f, 0.f};
+        h8 xnh[H16 ? MT : 1][H16 ? KG / 2 : 1];
+        if constexpr (H16) {
+#pragma unroll
+            for (int i = 0; i < MT; ++i)
+#pragma unroll
+                for (int kk = 0; kk < KG / 2; ++kk) xnh[i][kk] = pack8(xn[i][2 * kk], xn[i][2 * kk + 1]);
+        }
 #pragma unroll 1
         for (int ch = 0; ch < HID / HC; ++ch) {
             f4 acc1[HT][MT];
@@ -2420,16 +2714,27 @@ __global__ __launch_bounds__(T * 2) __attribute__((amdgpu_waves_per_eu(2, 2))) v
             for (int ht = 0; ht < HT; ++ht)
 #pragma unroll
                 for (int i = 0; i < MT; ++i) acc1[ht][i] = f4{0.f, 0.f, 0.f, 0.f};
+            if constexpr (H16) {
 #pragma unroll
-            for (int kg = 0; kg < KG; ++kg)
+                for (int kk = 0; kk < KG / 2; ++kk)
 #pragma unroll
-                for (int ht = 0; ht < HT; ++ht) {
-                    const f4 wv = ld4(a.w0 + long(ch * HC + ht * 16 + li) * T + kg * 16 + lg * 4);
+                    for (int ht = 0; ht < HT; ++ht) {
+                        const h8 wv = ldh8(a.h0 + long(ch * HC + ht * 16 + li) * T + kk * 32 + lg * 8);
 #pragma unroll
-                    for (int s4 = 0; s4 < 4; ++s4)
+                        for (int i = 0; i < MT; ++i) acc1[ht][i] = mfma16(wv, xnh[i][kk], acc1[ht][i]);
+                    }
+            } else {
 #pragma unroll
-                        for (int i = 0; i < MT; ++i) acc1[ht][i] = mfma4(wv[s4], xn[i][kg][s4], acc1[ht][i]);
-                }
+                for (int kg = 0; kg < KG; ++kg)
+#pragma unroll
+                    for (int ht = 0; ht < HT; ++ht) {
+                        const f4 wv = ld4(a.w0 + long(ch * HC + ht * 16 + li) * T + kg * 16 + lg * 4);
+#pragma unroll
+                        for (int s4 = 0; s4 < 4; ++s4)
+#pragma unroll
+                            for (int i = 0; i < MT; ++i) acc1[ht][i] = mfma4(wv[s4], xn[i][kg][s4], acc1[ht][i]);
+                    }
+            }
 #pragma unroll
             for (int ht = 0; ht < HT; ++ht) {
                 const f4 bb = ld4(a.b0 + ch * HC + ht * 16 + lg * 4);
@@ -2438,16 +2743,27 @@ __global__ __launch_bounds__(T * 2) __attribute__((amdgpu_waves_per_eu(2, 2))) v
 #pragma unroll
                     for (int r = 0; r < 4; ++r) acc1[ht][i][r] = gelu_as(acc1[ht][i][r] + bb[r]);
             }
+            if constexpr (H16) {
+                // HC = 32 hidden units: k block ch of W2.
 #pragma unroll
-            for (int ht = 0; ht < HT; ++ht)
+                for (int i = 0; i < MT; ++i) {
+                    const h8 hv = pack8(acc1[0][i], acc1[1][i]);
 #pragma unroll
-                for (int nt = 0; nt < KG; ++nt) {
-                    const f4 wv = ld4(a.w2 + long(nt * 16 + li) * HID + ch * HC + ht * 16 + lg * 4);
-#pragma unroll
-                    for (int r = 0; r < 4; ++r)
-#pragma unroll
-                        for (int i = 0; i < MT; ++i) acc2[i][nt] = mfma4(wv[r], acc1[ht][i][r], acc2[i][nt]);
+                    for (int nt = 0; nt < KG; ++nt)
+                        acc2[i][nt] = mfma16(ldh8(a.h2 + long(nt * 16 + li) * HID + ch * 32 + lg * 8), hv, acc2[i][nt]);
                 }
+            } else {
+#pragma unroll
+                for (int ht = 0; ht < HT; ++ht)
+#pragma unroll
+                    for (int nt = 0; nt < KG; ++nt) {
+                        const f4 wv = ld4(a.w2 + long(nt * 16 + li) * HID + ch * HC + ht * 16 + lg * 4);
+#pragma unroll
+                        for (int r = 0; r < 4; ++r)
+#pragma unroll
+                            for (int i = 0; i < MT; ++i) acc2[i][nt] = mfma4(wv[r], acc1[ht][i][r], acc2[i][nt]);
+                    }
+            }
         }
 #pragma unroll
         for (int i = 0; i < MT; ++i) {
@@ -2457,28 +2773,40 @@ __global__ __launch_bounds__(T * 2) __attribute__((amdgpu_waves_per_eu(2, 2))) v
                 st4(a.x + row * a.ldx + nt * 16 + lg * 4, xr[i][nt] + (acc2[i][nt] + ld4(a.b2 + nt * 16 + lg * 4)));
         }
     }
-}bool msa_fused(const MsaArgs& a, hipStream_t s, const char** why) {
-    const long nw = long(a.nwh) * a.nww;
-    if (nw == 0) return true;
+}
+
+template <bool H16>
+static bool launch_msa(const MsaArgs& a, long nw, hipStream_t s, const char** why) {
     dim3 grid{unsigned((nw + 3) / 4), 1u, 1u}, block{256u, 1u, 1u};
-    if (a.w0 && a.t != 32 && a.t != 64) {
-        *why = "msa_fused: the fused MLP is available at t = 32, 64";
-        return false;
-    }
-    if (a.t == 32 && a.w0) hipLaunchKernelGGL((k_msa<32, true>), grid, block, 0, s, a, nw);
-    else if (a.t == 32) hipLaunchKernelGGL((k_msa<32, false>), grid, block, 0, s, a, nw);
-    else if (a.t == 64 || a.t == 128 || a.t == 256) {
-        dim3 wgrid{unsigned(nw), 1u, 1u}, wblock{unsigned(a.t * 2), 1u, 1u};
-        if (a.t == 64 && a.w0) hipLaunchKernelGGL((k_wmsa<64, true>), wgrid, wblock, 0, s, a, nw);
-        else if (a.t == 64) hipLaunchKernelGGL((k_wmsa<64, false>), wgrid, wblock, 0, s, a, nw);
-        else if (a.t == 128) hipLaunchKernelGGL((k_wmsa<128, false>), wgrid, wblock, 0, s, a, nw);
-        else hipLaunchKernelGGL((k_wmsa<256, false>), wgrid, wblock, 0, s, a, nw);
-    }
+    dim3 wgrid{unsigned(nw), 1u, 1u}, wblock{unsigned(a.t * 2), 1u, 1u};
+    if (a.t == 32 && a.w0) hipLaunchKernelGGL((k_msa<32, true, H16>), grid, block, 0, s, a, nw);
+    else if (a.t == 32) hipLaunchKernelGGL((k_msa<32, false, H16>), grid, block, 0, s, a, nw);
+    else if (a.t == 64 && a.w0) hipLaunchKernelGGL((k_wmsa<64, true, H16>), wgrid, wblock, 0, s, a, nw);
+    else if (a.t == 64) hipLaunchKernelGGL((k_wmsa<64, false, H16>), wgrid, wblock, 0, s, a, nw);
+    else if (a.t == 128) hipLaunchKernelGGL((k_wmsa<128, false, H16>), wgrid, wblock, 0, s, a, nw);
+    else if (a.t == 256) hipLaunchKernelGGL((k_wmsa<256, false, H16>), wgrid, wblock, 0, s, a, nw);
     else {
         *why = "msa_fused: t must be 32, 64, 128 or 256";
         return false;
     }
     return true;
+}
+
+bool msa_fused(const MsaArgs& a, hipStream_t s, const char** why) {
+    const long nw = long(a.nwh) * a.nww;
+    if (nw == 0) return true;
+    if (a.w0 && a.t != 32 && a.t != 64) {
+        *why = "msa_fused: the fused MLP is available at t = 32, 64";
+        return false;
+    }
+    if (a.hqkv) {
+        if (!a.hp || (a.w0 && (!a.h0 || !a.h2))) {
+            *why = "msa_fused: the fp16 path needs every k-permuted weight it uses";
+            return false;
+        }
+        return launch_msa<true>(a, nw, s, why);
+    }
+    return launch_msa<false>(a, nw, s, why);
 }
 
 void build_bias_table(const float* rp, int heads, float* tab) {
@@ -2677,6 +3005,25 @@ void nchw_to_nhwc(const float* src, float* dst, int c, long P, long ld, hipStrea
 void nhwc_to_nchw(const float* src, float* dst, int c, long P, long ld, hipStream_t s) {
     dim3 grid(unsigned((P + 31) / 32), unsigned((c + 31) / 32));
     hipLaunchKernelGGL(k_nhwc_to_nchw, grid, dim3(256), 0, s, src, dst, c, P, ld);
+}
+
+// The k-permuted fp16 copy of a weight matrix [rows][K] (K % 32 == 0): output chunk
+// q = 4 b + g of a row (8 halves) packs k = 32 b + 4 g .. + 3 and 32 b + 16 + 4 g .. + 3.
+__global__ void k_h16_permute(const float* __restrict__ src, _Float16* __restrict__ dst, long rows, int K) {
+    const long n = rows * (K / 8);
+    for (long i = long(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += long(gridDim.x) * blockDim.x) {
+        const long row = i / (K / 8);
+        const int q = int(i - row * (K / 8));
+        const float* p = src + row * K + 32 * (q >> 2) + 4 * (q & 3);
+        sth8(dst + row * K + q * 8, pack8(ld4(p), ld4(p + 16)));
+    }
+}
+
+void h16_permute(const float* src, half_t* dst, long rows, int K, hipStream_t s) {
+    const long n = rows * (K / 8);
+    if (n <= 0) return;
+    dim3 grid{unsigned(std::min<long>((n + 255) / 256, 4096)), 1u, 1u}, block{256u, 1u, 1u};
+    hipLaunchKernelGGL(k_h16_permute, grid, block, 0, s, src, dst, rows, K);
 }
 
 __global__ void k_copy_f4(const f4* __restrict__ src, f4* __restrict__ dst, long n) {

@@ -23,7 +23,8 @@ LIB_PATH = os.path.join(_HERE, "..", "lib", "libscunet_hip.so")
 # The symbols include/scunet_hip.h declares.
 EXPORTS = [
     "scunet_hip_create", "scunet_hip_create_error", "scunet_hip_destroy", "scunet_hip_last_error",
-    "scunet_hip_name", "scunet_hip_arch", "scunet_hip_forward", "scunet_hip_forward_device",
+    "scunet_hip_name", "scunet_hip_arch", "scunet_hip_set_precision", "scunet_hip_precision",
+    "scunet_hip_forward", "scunet_hip_forward_device",
     "scunet_hip_forward_dump", "scunet_hip_run", "scunet_hip_run_device", "scunet_hip_footprint",
     "scunet_hip_release_scratch", "scunet_hip_synchronize", "scunet_hip_stream", "scunet_hip_profile",
     "scunet_hip_profile_report", "scunet_hip_malloc", "scunet_hip_free", "scunet_hip_h2d", "scunet_hip_d2h",
@@ -64,6 +65,8 @@ def load_library(path=None):
     L.scunet_hip_name.restype = ctypes.c_char_p
     ip = ctypes.POINTER(ctypes.c_int)
     L.scunet_hip_arch.argtypes = [_vp, ip, ip, ip, ip, ip]
+    L.scunet_hip_set_precision.argtypes = [_vp, ctypes.c_int]
+    L.scunet_hip_precision.argtypes = [_vp]
     L.scunet_hip_forward.argtypes = [_vp, _f, _sz, _sz, _sz, _f]
     L.scunet_hip_forward_device.argtypes = [_vp, _vp, _sz, _sz, _sz, _vp]
     L.scunet_hip_forward_dump.argtypes = [_vp, _f, _sz, _sz, _sz, _f, HOOK, _vp]
@@ -197,6 +200,18 @@ class Hip:
     # -- trait Backend --
     def name(self):
         return self._lib.scunet_hip_name(self._h).decode()
+
+    # -- arithmetic mode (no counterpart in the reference) --
+    PRECISIONS = {"fp32": 0, "fp16": 1}
+
+    def set_precision(self, mode):
+        """"fp32" (the reference's arithmetic, the default) or "fp16" (fp16 MFMA operands,
+        fp32 accumulation and planes)."""
+        self._check(self._lib.scunet_hip_set_precision(self._h, self.PRECISIONS[mode]))
+
+    def precision(self):
+        m = self._lib.scunet_hip_precision(self._h)
+        return {v: k for k, v in self.PRECISIONS.items()}[m]
 
     def forward(self, x, plan):
         """backend.rs:23-25: padded [c][hp][wp] in, a fresh [c][hp][wp] out."""

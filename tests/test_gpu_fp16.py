@@ -1,0 +1,110 @@
+"""The fp16-operand mode (scunet_hip_set_precision(h, SCUNET_HIP_FP16)): matrix products
+take fp16 operands with fp32 accumulation; planes, residuals, LayerNorm, softmax and GELU
+stay fp32. The reference has no such mode, so it is held to its own stated tolerance
+against the reference's fp32 arithmetic (the oracle) and against this library's fp32 mode:
+
+    FP16_MAX_ABS = 4e-3 per stage plane and on the output (|plane| <= ~2.5 here);
+    FP16_PSNR_DB = 70 dB on the output image (peak 1), against fp32.
+
+An fp16 operand carries a relative rounding error of at most 2^-11 (4.9e-4); with fp32
+accumulation the error of a K-term product grows like sqrt(K) times that relative to the
+product's own magnitude, which is what the per-stage figures here show (~2e-4 .. 5e-4 of
+the plane's scale). The fp32 mode must be unaffected by having used the fp16 mode."""
+import numpy as np
+import pytest
+
+import oracle as O
+from conftest import max_abs
+
+pytestmark = pytest.mark.gpu
+
+FP16_MAX_ABS = 4e-3
+FP16_PSNR_DB = 70.0
+STAGE_TOL = 1e-4
+
+
+def psnr(want, got):
+    d = np.asarray(want, np.float64) - np.asarray(got, np.float64)
+    mse = float(np.mean(d * d))
+    return float("inf") if mse == 0.0 else 10.0 * np.log10(1.0 / mse)
+
+
+@pytest.fixture(scope="module")
+def be16(weights_path):
+    from scunet_hip import Hip
+    h = Hip(weights_path)
+    h.set_precision("fp16")
+    yield h
+    h.close()
+
+
+def test_precision_switch(weights_path):
+    from scunet_hip import BackendError, Hip
+    with Hip(weights_path) as be:
+        assert be.precision() == "fp32"
+        w32, _ = be.footprint()
+        be.set_precision("fp16")
+        assert be.precision() == "fp16"
+        w16, _ = be.footprint()
+        # The fp16 weight copies: at most half the fp32 bytes again.
+        assert w32 < w16 <= w32 + w32 // 2 + (1 << 20)
+        be.set_precision("fp32")
+        assert be.precision() == "fp32"
+        with pytest.raises(BackendError, match="mode must be"):
+            be._check(be._lib.scunet_hip_set_precision(be._h, 7))
+        assert be.precision() == "fp32"
+
+
+def test_fp16_every_stage_within_tolerance_at_64x64(be16, owt, golden):
+    x = golden["fwd64_in"]
+    _, want = O.forward_dump(owt, x)
+    got = {}
+    y = be16.forward_dump(x, lambda n, v: got.__setitem__(n, v))
+    assert list(got) == list(want)
+    worst = 0.0
+    for name in want:
+        d = max_abs(want[name], got[name])
+        assert d <= FP16_MAX_ABS, f"{name}: {d:.3e}"
+        worst = max(worst, d)
+    # Not the fp32 path in disguise: fp16 operands leave a visible, bounded difference.
+    assert worst > STAGE_TOL / 10
+    assert psnr(want["m_tail"], y) >= FP16_PSNR_DB
+
+
+@pytest.mark.parametrize("prefix,h,w,shift", [("m_down1.1", 24, 40, 4), ("m_down2.2", 16, 32, 0),
+                                              ("m_down3.1", 16, 16, 4), ("m_body.0", 8, 16, 0),
+                                              ("m_up2.2", 32, 16, 4)])
+def test_fp16_block_within_tolerance(be16, owt, prefix, h, w, shift):
+    c = sum(owt.block_dims(prefix))
+    rng = np.random.default_rng(h * 1000 + w * 10 + shift)
+    x = rng.standard_normal((c, h, w)).astype(np.float32)
+    want = O.conv_trans_block(owt, prefix, x, shift)
+    got = be16.block_dump(prefix, h, w, shift, x)
+    scale = float(np.abs(want).max())
+    assert max_abs(want, got) <= FP16_MAX_ABS * max(1.0, scale), prefix
+
+
+def test_fp16_config2_512_against_cpu(be16, owt):
+    from scunet_hip import synth
+    x = synth.config_input(2)
+    want = O.run(owt, x)
+    got = be16.run_fused(x)
+    assert max_abs(want, got) <= FP16_MAX_ABS
+    assert psnr(want, got) >= FP16_PSNR_DB
+
+
+def test_fp16_1080p_against_fp32_mode(weights_path):
+    """At the headline size (config 3) the fp16 output against the fp32 mode's output,
+    which is itself within 1e-4 of the reference arithmetic; switching back gives the fp32
+    result bit for bit."""
+    from scunet_hip import Hip, synth
+    x = synth.config_input(3)
+    with Hip(weights_path) as be:
+        y32 = be.run_fused(x)
+        be.set_precision("fp16")
+        y16 = be.run_fused(x)
+        be.set_precision("fp32")
+        y32b = be.run_fused(x)
+    assert np.array_equal(y32, y32b)
+    assert max_abs(y32, y16) <= FP16_MAX_ABS
+    assert psnr(y32, y16) >= FP16_PSNR_DB
