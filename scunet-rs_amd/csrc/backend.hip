@@ -317,7 +317,11 @@ bool run_conv3(scunet_hip* h, const std::string& name, Conv3Args c, bool relu) {
             4.0 * (double(P) * (c.cin + c.cout * (relu ? 1 : 2)) + 9.0 * c.cin * c.cout));
     const char* why = nullptr;
     const float* u = W(h, "@wino:" + name + ".weight");
-    if (!h->direct3x3 && u && c.cin % 16 == 0 && c.cout % 16 == 0 && c.H % 2 == 0 && c.W % 2 == 0) {
+    const half_t* w16 = W16(h, name + ".weight");
+    if (w16 && c.cin == c.cout && (c.cin == 32 || c.cin == 64 || c.cin == 128 || c.cin == 256)) {
+        c.w16 = w16;
+        if (!conv3x3_h16(c, relu, h->stream, &why)) return fail(h, why);
+    } else if (!h->direct3x3 && u && c.cin % 16 == 0 && c.cout % 16 == 0 && c.H % 2 == 0 && c.W % 2 == 0) {
         c.w = u;
         c.cblock = h->wino16 ? 16 : 0;
         if (!conv3x3_winograd(c, relu, h->stream, &why)) return fail(h, why);

@@ -114,12 +114,16 @@ struct Conv3Args {
     long ldo = 0;
     int H = 0, W = 0, cin = 0, cout = 0;
     int cblock = 0;                // Winograd: output channels per unit (0 = 32 when possible, 16)
+    const half_t* w16 = nullptr;   // fp16 mode: [9][cout][cin] k-permuted (conv3x3_h16)
 };
 // relu=true: out = relu(conv); relu=false: out += conv (the conv half's residual).
 bool conv3x3(const Conv3Args& a, bool relu, hipStream_t s, const char** why);
 // The same convolution by Winograd F(2x2, 3x3); a.w is the transformed filter
 // U = G g G^T laid out [16][cout][cin] (see winograd_filter). cin, cout multiples of 16.
 bool conv3x3_winograd(const Conv3Args& a, bool relu, hipStream_t s, const char** why);
+// The fp16-operand direct convolution, cin = cout in {32, 64, 128, 256}; a.w16 holds the
+// filters [9][cout][cin] k-permuted (a.w is not read).
+bool conv3x3_h16(const Conv3Args& a, bool relu, hipStream_t s, const char** why);
 // Host-side filter transform: g [cout][cin][3][3] -> U [16][cout][cin] (in double).
 void winograd_filter(const float* g, int cout, int cin, float* u);
 

@@ -1796,6 +1796,150 @@ bool conv3x3_winograd(const Conv3Args& a, bool relu, hipStream_t s, const char**
     return true;
 }
 
+// ---------------------------------------------------------------------------
+// The fp16-operand 3x3 convolution (cin = cout = C), a direct implicit GEMM:
+// out^T[co][px] = sum over taps (ky, kx) and ci of W[ky*3+kx][co][ci] in[px + (ky-1, kx-1)][ci].
+// With fp16 products 16x cheaper than fp32 ones, the transforms of the Winograd form would
+// cost more than the multiplications they save, so this form does 2.25x the products and
+// no transforms.
+//   - A workgroup owns an R-row x TW-column output tile. Its (R+2) x (TW+2) halo, all C
+//     channels, is staged once into LDS as fp16: each 16-byte slot q = 4b + g of a pixel
+//     packs channels 32b + 4g .. + 3 and 32b + 16 + 4g .. + 3, the k order of the f16
+//     product, so a thread's two float4 loads convert straight into one slot. Pixels are
+//     SP + 2 slots apart (SP = C / 8): 16 consecutive pixels x 2 slots land on distinct
+//     16-byte slots mod 32, so operand reads are conflict-free, and every read is a fixed
+//     per-lane base plus a compile-time offset.
+//   - Wave w computes 32 output channels (co-group w % (C/32)) of a 16-pixel-wide strip
+//     (w / (C/32)) for all R rows. Each halo-row fragment (16 pixels x 32 channels) read
+//     for horizontal tap kx serves the output rows it is the ky = 0, 1, 2 tap of: 3 rows x
+//     2 channel tiles of products per read.
+//   - The k-permuted fp16 filters come from global memory: all of them held in registers
+//     for C <= 64, else one 32-channel block at a time with the next block's loads in
+//     flight during the current block's products.
+// ---------------------------------------------------------------------------
+template <int C, int R, int NWV, bool RELU>
+__global__ __launch_bounds__(NWV * 64) void k_conv3h(Conv3Args a, int tiles_x, long tiles) {
+    constexpr int CG = C / 32, KK = C / 32;
+    static_assert(NWV % CG == 0, "the waves split into whole co-groups");
+    constexpr int STRIPS = NWV / CG, TW = 16 * STRIPS, RP = TW + 2;
+    constexpr int SP = C / 8, SPP = SP + 2;
+    constexpr bool WRES = KK <= 2;                 // every filter block resident
+    constexpr int NA = WRES ? KK : 2;              // filter blocks held (resident, or double buffer)
+    __shared__ __align__(16) _Float16 halo[(R + 2) * RP * SPP * 8];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int li = lane & 15, lg = lane >> 4;
+    const int cog = wave % CG, strip = wave / CG;
+    const long ti = xcd_swizzle(blockIdx.x, gridDim.x);
+    if (ti >= tiles) return;   // no barrier is reached by any wave of this workgroup
+    const int ty = int(ti / tiles_x), tx = int(ti - long(ty) * tiles_x);
+    const int y0 = ty * R, x0 = tx * TW;
+
+    // Filter fragments: A[tap][j] = W[tap][cog*32 + 16j + li][32kk + 8lg .. (k-permuted)].
+    h8 wa[NA][9][2];
+    auto wload = [&](int kk, h8 (&dst)[9][2]) {
+#pragma unroll
+        for (int tap = 0; tap < 9; ++tap)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+                dst[tap][j] = ldh8(a.w16 + (long(tap * C + cog * 32 + j * 16 + li) * C + kk * 32 + lg * 8));
+    };
+#pragma unroll
+    for (int k = 0; k < NA; ++k) wload(k, wa[k]);
+
+    // Stage the halo (zero outside the plane: the convolution's zero padding).
+    constexpr int NSLOT = (R + 2) * RP * SP;
+    for (int f = tid; f < NSLOT; f += NWV * 64) {
+        const int q = f % SP, p = f / SP;
+        const int hr = p / RP, hc = p - hr * RP;
+        const int gy = y0 - 1 + hr, gx = x0 - 1 + hc;
+        h8 v = h8{0, 0, 0, 0, 0, 0, 0, 0};
+        if (gy >= 0 && gy < a.H && gx >= 0 && gx < a.W) {
+            const float* src = a.in + (long(gy) * a.W + gx) * a.ldi + 32 * (q >> 2) + 4 * (q & 3);
+            v = pack8(ld4(src), ld4(src + 16));
+        }
+        sth8(halo + (p * SPP + q) * 8, v);
+    }
+    __syncthreads();
+
+    f4 acc[R][2];
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r][0] = acc[r][1] = f4{0.f, 0.f, 0.f, 0.f};
+    const _Float16* hb = halo + ((strip * 16 + li) * SPP + lg) * 8;
+    auto block = [&](int kk, const h8 (&w)[9][2]) {
+#pragma unroll
+        for (int dx = 0; dx < 3; ++dx)
+#pragma unroll
+            for (int hr = 0; hr < R + 2; ++hr) {
+                const h8 b = ldh8(hb + ((hr * RP + dx) * SPP + kk * 4) * 8);
+#pragma unroll
+                for (int dy = 0; dy < 3; ++dy) {
+                    const int r = hr - dy;
+                    if (r < 0 || r >= R) continue;
+#pragma unroll
+                    for (int j = 0; j < 2; ++j) acc[r][j] = mfma16(w[dy * 3 + dx][j], b, acc[r][j]);
+                }
+            }
+    };
+    if constexpr (WRES) {
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk) block(kk, wa[kk]);
+    } else {
+#pragma unroll 1
+        for (int kk = 0; kk < KK; kk += 2) {
+            block(kk, wa[0]);
+            if (kk + 2 < KK) wload(kk + 2, wa[0]);
+            block(kk + 1, wa[1]);
+            if (kk + 3 < KK) wload(kk + 3, wa[1]);
+        }
+    }
+
+    // Lanes hold output channels cog*32 + 16j + 4lg .. + 3 of pixel (y0 + r, x0 + 16 strip + li).
+    const int x = x0 + strip * 16 + li;
+    if (x >= a.W) return;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int y = y0 + r;
+        if (y >= a.H) break;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            float* o = a.out + (long(y) * a.W + x) * a.ldo + cog * 32 + j * 16 + lg * 4;
+            if constexpr (RELU) {
+                const f4 v = acc[r][j];
+                st4(o, f4{fmaxf(v.x, 0.f), fmaxf(v.y, 0.f), fmaxf(v.z, 0.f), fmaxf(v.w, 0.f)});
+            } else {
+                st4(o, ld4(o) + acc[r][j]);
+            }
+        }
+    }
+}
+
+template <int C, int R, int NWV>
+static void launch_conv3h(const Conv3Args& a, bool relu, hipStream_t s) {
+    constexpr int TW = 16 * (NWV / (C / 32));
+    const int tiles_x = (a.W + TW - 1) / TW;
+    const long tiles = long(tiles_x) * ((a.H + R - 1) / R);
+    dim3 grid{unsigned(tiles), 1u, 1u}, block{unsigned(NWV * 64), 1u, 1u};
+    if (relu) hipLaunchKernelGGL((k_conv3h<C, R, NWV, true>), grid, block, 0, s, a, tiles_x, tiles);
+    else hipLaunchKernelGGL((k_conv3h<C, R, NWV, false>), grid, block, 0, s, a, tiles_x, tiles);
+}
+
+bool conv3x3_h16(const Conv3Args& a, bool relu, hipStream_t s, const char** why) {
+    if (!a.w16 || a.cin != a.cout) {
+        *why = "conv3x3_h16: needs the k-permuted fp16 filters and cin == cout";
+        return false;
+    }
+    if (a.H <= 0 || a.W <= 0) return true;
+    switch (a.cin) {
+        case 32: launch_conv3h<32, 8, 4>(a, relu, s); break;
+        case 64: launch_conv3h<64, 8, 4>(a, relu, s); break;
+        case 128: launch_conv3h<128, 8, 4>(a, relu, s); break;
+        case 256: launch_conv3h<256, 4, 8>(a, relu, s); break;
+        default: *why = "conv3x3_h16: channels must be 32, 64, 128 or 256"; return false;
+    }
+    return true;
+}
+
 void winograd_filter(const float* g, int cout, int cin, float* u) {
     static const double G[4][3] = {{1, 0, 0}, {0.5, 0.5, 0.5}, {0.5, -0.5, 0.5}, {0, 0, 1}};
     for (int o = 0; o < cout; ++o)

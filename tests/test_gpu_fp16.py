@@ -24,7 +24,7 @@ STAGE_TOL = 1e-4
 
 
 def psnr(want, got):
-    d = np.asarray(want, np.float64) - np.asarray(got, np.float64)
+    d = np.asarray(want, np.float64).ravel() - np.asarray(got, np.float64).ravel()
     mse = float(np.mean(d * d))
     return float("inf") if mse == 0.0 else 10.0 * np.log10(1.0 / mse)
 
