@@ -130,6 +130,7 @@ def main():
     ap.add_argument("--no-kernel-events", action="store_true",
                     help="time the steps without the per-launch event pairs")
     ap.add_argument("--no-attn-sweep", action="store_true", help="skip the config-5 attention sweep")
+    ap.add_argument("--no-fp16", action="store_true", help="skip the fp16-operand mode's line")
     ap.add_argument("--profile-pass", action="store_true",
                     help="for rocprofv3 counter runs: one forward plus one 256 MiB device copy (the "
                          "calibration kernel), nothing else; prints no JSON line")
@@ -206,6 +207,33 @@ def main():
         h2h.append(time.perf_counter() - t1)
     h2h_med = sorted(h2h)[1]
     log(f"bench: host to host (scunet_hip_run, PCIe included) {h2h_med * 1e3:.2f} ms, {h * w / h2h_med / 1e6:.2f} Mpx/s")
+    fp = be.footprint()
+
+    # The fp16-operand mode (fp16 MFMA operands, fp32 accumulation and planes), reported
+    # beside the fp32 headline with its error against the fp32 output of the same input.
+    fp16 = None
+    if not args.no_fp16:
+        be.set_precision("fp16")
+        for _ in range(args.warmup):
+            be.run_device(xp, c, h, w, yp)
+        be.synchronize()
+        t1 = time.perf_counter()
+        for _ in range(args.steps):
+            be.run_device(xp, c, h, w, yp)
+        be.synchronize()
+        dt16 = (time.perf_counter() - t1) / args.steps
+        y16 = be.d2h(np.empty_like(x), yp)
+        be.set_precision("fp32")
+        d = y16.astype(np.float64) - y.astype(np.float64)
+        mse = float(np.mean(d * d))
+        fp16 = {"value": round(h * w / dt16 / 1e6, 3), "unit": "Mpx/s", "ms_per_step": round(dt16 * 1e3, 3),
+                "max_abs_vs_fp32": float(np.abs(d).max()),
+                "psnr_db_vs_fp32": round(10 * np.log10(1.0 / mse), 2) if mse > 0 else None,
+                "tolerance": {"max_abs": 4e-3, "psnr_db": 70.0},
+                "note": "scunet_hip_set_precision(SCUNET_HIP_FP16): fp16 MFMA operands, fp32 accumulation, "
+                        "fp32 planes/LayerNorm/softmax/GELU; not the headline (the reference path is fp32)"}
+        log(f"bench: fp16 mode {dt16 * 1e3:.2f} ms/step, {fp16['value']:.2f} Mpx/s, max |diff| vs fp32 "
+            f"{fp16['max_abs_vs_fp32']:.2e}, PSNR {fp16['psnr_db_vs_fp32']} dB")
 
     # Rows are per (kernel class, UNet level "@Lk"); aggregate per class for the roofline.
     total_ms = max(sum(r[2] for r in rows), 1e-9)
@@ -273,7 +301,6 @@ def main():
         cpu = cpu_baseline(wpath, x, args.cpu_rows)
         log(f"bench: CPU baseline {cpu['value']} Mpx/s on {cpu['cores']} threads ({cpu['seconds']} s)")
 
-    fp = be.footprint()
     line = {
         "metric": METRIC,
         "value": round(mpx, 3),
@@ -303,6 +330,7 @@ def main():
         "host_to_host": {"ms": round(h2h_med * 1e3, 3), "mpx_s": round(h * w / h2h_med / 1e6, 3),
                          "note": "scunet_hip_run on host buffers: H2D + pad + forward + crop + D2H, median of 3"},
         "device_bytes": {"weights": fp[0], "scratch": fp[1]},
+        "fp16_mode": fp16,
     }
     be.free(xp)
     be.free(yp)

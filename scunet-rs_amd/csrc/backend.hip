@@ -70,6 +70,7 @@ struct scunet_hip {
     half_t* h16blob = nullptr;
     size_t h16bytes = 0;
     std::map<std::string, const half_t*> hw;
+    std::map<const float*, const half_t*> hw_of;   // fp32 device pointer -> its fp16 copy
     std::string tag;                     // appended to profiler class names ("@L0".."@L3")
     std::vector<ProfRec> recs;
     std::vector<hipEvent_t> ev_pool;
@@ -288,6 +289,7 @@ bool build_h16_weights(scunet_hip* h) {
         h16_permute(it.src, reinterpret_cast<half_t*>(at), it.rows, it.K, h->stream);
         if (!launched(h, "fp16 weights")) return false;
         h->hw[it.name] = reinterpret_cast<const half_t*>(at);
+        h->hw_of[it.src] = reinterpret_cast<const half_t*>(at);
         at += (size_t(it.rows) * it.K * 2 + 255) / 256 * 256;
     }
     return ck(h, hipStreamSynchronize(h->stream), "fp16 weights");
@@ -304,6 +306,10 @@ bool run_gemm(scunet_hip* h, const char* cls, const GemmArgs& g, GemmA a, GemmE 
     const char* why = nullptr;
     GemmArgs gg = g;
     gg.persistent = h->gemm2 ? 0 : 1;
+    if (h->h16 && !h->gemm2) {
+        auto it = h->hw_of.find(g.W);
+        if (it != h->hw_of.end()) gg.W16 = it->second;
+    }
     if (!gemm(gg, a, e, h->stream, &why)) return fail(h, std::string(cls) + ": " + why);
     return launched(h, cls);
 }

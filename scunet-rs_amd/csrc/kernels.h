@@ -57,6 +57,9 @@ struct GemmArgs {
     int cin = 0;    // A_S2D
     int cout = 0;   // E_D2S
     int persistent = 1;   // the persistent tile walker for non-LN operands (0: one tile per workgroup)
+    // fp16 mode: W k-permuted. Used by the persistent walker for N % 64 == 0, K % 32 == 0 and
+    // the row, patch and skip-sum operands; other shapes keep fp32 products.
+    const half_t* W16 = nullptr;
 };
 
 // Returns false (and a reason) if no tile configuration fits the shape.

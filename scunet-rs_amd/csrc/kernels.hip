@@ -452,14 +452,19 @@ __global__ __launch_bounds__(256) void k_gemm2(GemmArgs g) {
 // double-buffered in LDS; the epilogue uses registers only). Tile t = 8 j + xcd: the
 // N-blocks of one M-tile are consecutive j on one XCD and share its L2.
 // ---------------------------------------------------------------------------
-template <int MT, int BN, int KC, int AM, int EP>
+template <int MT, int BN, int KC, int AM, int EP, bool H16>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_gemm3(GemmArgs g, long tiles) {
-    constexpr int NT = BN / 16, KG = KC / 16, LDB = KC + 8;
-    constexpr int BV = BN * KC / 4 / 256;
-    static_assert(BN * KC / 4 % 256 == 0, "weight slice must split evenly over 256 threads");
+    // fp16 mode: a K slice is one 32-wide k block of the k-permuted weights, staged as halves
+    // with rows of 48 (2 mod 4 sixteen-byte slots: conflict-free 128-bit reads).
+    static_assert(!H16 || KC == 32, "fp16 slices are one k block");
+    constexpr int NT = BN / 16, KG = KC / 16, LDB = H16 ? 48 : KC + 8;
+    constexpr int EV = H16 ? 8 : 4;               // elements per 16-byte chunk
+    constexpr int BV = BN * KC / EV / 256;
+    static_assert(BN * KC / EV % 256 == 0, "weight slice must split evenly over 256 threads");
     // The residual is read ahead when its registers fit (up to 8 float4 per lane).
     constexpr bool RPRE = EP == E_RESID && MT * NT <= 8;
-    __shared__ float Bs[2 * BN * LDB];
+    using ET = std::conditional_t<H16, _Float16, float>;
+    __shared__ __align__(16) ET Bs[2 * BN * LDB];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int li = lane & 15, lg = lane >> 4;
@@ -490,16 +495,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
         for (int i = 0; i < BV; ++i) {
             const int f = tid + i * 256;
-            const int row = f / (KC / 4), c4 = f % (KC / 4);
-            bpre[i] = ld4(g.W + long(n0 + row) * g.K + k0 + c4 * 4);
+            const int row = f / (KC / EV), c = f % (KC / EV);
+            if constexpr (H16) bpre[i] = ld4(reinterpret_cast<const float*>(g.W16 + long(n0 + row) * g.K + k0 + c * 8));
+            else bpre[i] = ld4(g.W + long(n0 + row) * g.K + k0 + c * 4);
         }
     };
     auto bstore = [&](int b) {
 #pragma unroll
         for (int i = 0; i < BV; ++i) {
             const int f = tid + i * 256;
-            const int row = f / (KC / 4), c4 = f % (KC / 4);
-            st4(&Bs[b * BN * LDB + row * LDB + c4 * 4], bpre[i]);
+            const int row = f / (KC / EV), c = f % (KC / EV);
+            st4(reinterpret_cast<float*>(&Bs[b * BN * LDB + row * LDB + c * EV]), bpre[i]);
         }
     };
     f4 acur[MT][KG], anext[MT][KG];
@@ -552,18 +558,30 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                     }
                 }
             }
-            const float* B = Bs + kb * BN * LDB;
+            const ET* B = Bs + kb * BN * LDB;
+            if constexpr (H16) {
+                h8 ap[MT];
 #pragma unroll
-            for (int kg = 0; kg < KG; ++kg) {
-                f4 b[NT];
+                for (int mt = 0; mt < MT; ++mt) ap[mt] = pack8(acur[mt][0], acur[mt][1]);
 #pragma unroll
-                for (int nt = 0; nt < NT; ++nt) b[nt] = ld4(B + (nt * 16 + li) * LDB + kg * 16 + lg * 4);
+                for (int nt = 0; nt < NT; ++nt) {
+                    const h8 bh = ldh8(B + (nt * 16 + li) * LDB + lg * 8);
 #pragma unroll
-                for (int s4 = 0; s4 < 4; ++s4)
+                    for (int mt = 0; mt < MT; ++mt) acc[mt][nt] = mfma16(bh, ap[mt], acc[mt][nt]);
+                }
+            } else {
 #pragma unroll
-                    for (int mt = 0; mt < MT; ++mt)
+                for (int kg = 0; kg < KG; ++kg) {
+                    f4 b[NT];
 #pragma unroll
-                        for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = mfma4(b[nt][s4], acur[mt][kg][s4], acc[mt][nt]);
+                    for (int nt = 0; nt < NT; ++nt) b[nt] = ld4(B + (nt * 16 + li) * LDB + kg * 16 + lg * 4);
+#pragma unroll
+                    for (int s4 = 0; s4 < 4; ++s4)
+#pragma unroll
+                        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                            for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = mfma4(b[nt][s4], acur[mt][kg][s4], acc[mt][nt]);
+                }
             }
             if (more) bstore(kb ^ 1);
             __syncthreads();
@@ -609,14 +627,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     }
 }
 
-template <int MT, int BN, int KC, int AM, int EP>
+template <int MT, int BN, int KC, int AM, int EP, bool H16>
 static void launch_gemm3_k(const GemmArgs& g, hipStream_t s) {
     static int per_cu = -1, cus = 0;
     if (per_cu < 0) {
         int dev = 0;
         if (hipGetDevice(&dev) != hipSuccess ||
             hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_gemm3<MT, BN, KC, AM, EP>, 256, 0) != hipSuccess)
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_gemm3<MT, BN, KC, AM, EP, H16>, 256, 0) !=
+                hipSuccess)
             per_cu = 1;
         if (per_cu < 1) per_cu = 1;
         if (cus < 1) cus = 256;
@@ -624,17 +643,17 @@ static void launch_gemm3_k(const GemmArgs& g, hipStream_t s) {
     const long mtiles = (g.M + 64 * MT - 1) / (64 * MT);
     const long tiles = ((mtiles + 7) / 8) * 8 * (g.N / BN);
     dim3 grid{unsigned(std::min<long>(tiles, long(cus) * per_cu)), 1u, 1u}, block{256u, 1u, 1u};
-    hipLaunchKernelGGL((k_gemm3<MT, BN, KC, AM, EP>), grid, block, 0, s, g, tiles);
+    hipLaunchKernelGGL((k_gemm3<MT, BN, KC, AM, EP, H16>), grid, block, 0, s, g, tiles);
 }
 
-template <int MT, int BN, int KC, int AM>
+template <int MT, int BN, int KC, int AM, bool H16 = false>
 static void launch_gemm3_e(const GemmArgs& g, GemmE e, hipStream_t s) {
     switch (e) {
-        case E_STORE: launch_gemm3_k<MT, BN, KC, AM, E_STORE>(g, s); break;
-        case E_DUAL: launch_gemm3_k<MT, BN, KC, AM, E_DUAL>(g, s); break;
-        case E_GELU: launch_gemm3_k<MT, BN, KC, AM, E_GELU>(g, s); break;
-        case E_RESID: launch_gemm3_k<MT, BN, KC, AM, E_RESID>(g, s); break;
-        case E_D2S: launch_gemm3_k<MT, BN, KC, AM, E_D2S>(g, s); break;
+        case E_STORE: launch_gemm3_k<MT, BN, KC, AM, E_STORE, H16>(g, s); break;
+        case E_DUAL: launch_gemm3_k<MT, BN, KC, AM, E_DUAL, H16>(g, s); break;
+        case E_GELU: launch_gemm3_k<MT, BN, KC, AM, E_GELU, H16>(g, s); break;
+        case E_RESID: launch_gemm3_k<MT, BN, KC, AM, E_RESID, H16>(g, s); break;
+        case E_D2S: launch_gemm3_k<MT, BN, KC, AM, E_D2S, H16>(g, s); break;
     }
 }
 
@@ -647,7 +666,23 @@ static void launch_gemm3_a(const GemmArgs& g, GemmA a, GemmE e, hipStream_t s) {
     }
 }
 
+template <int MT, int BN>
+static void launch_gemm3_h16(const GemmArgs& g, GemmA a, GemmE e, hipStream_t s) {
+    switch (a) {
+        case A_ROWS: launch_gemm3_e<MT, BN, 32, A_ROWS, true>(g, e, s); break;
+        case A_S2D: launch_gemm3_e<MT, BN, 32, A_S2D, true>(g, e, s); break;
+        case A_ADD2: launch_gemm3_e<MT, BN, 32, A_ADD2, true>(g, e, s); break;
+        default: break;
+    }
+}
+
 static bool launch_gemm3(const GemmArgs& g, GemmA a, GemmE e, hipStream_t s) {
+    if (g.W16 && a != A_LN && g.K % 32 == 0 && g.N % 64 == 0) {
+        if (g.N <= 128) launch_gemm3_h16<2, 64>(g, a, e, s);
+        else if (g.N % 128 == 0) launch_gemm3_h16<2, 128>(g, a, e, s);
+        else launch_gemm3_h16<4, 64>(g, a, e, s);
+        return true;
+    }
     // The LayerNorm operand keeps its row in registers (k_gemm2); the skip-sum operand with
     // the depth-to-space epilogue measured faster one tile per workgroup (k_gemm2).
     if (a == A_LN || a == A_ADD2) return false;
