@@ -1001,8 +1001,9 @@ bool pconv(const PconvArgs& a, PconvMode mode, hipStream_t s, const char** why) 
 // H[row li][4 consecutive hidden units]: exactly the A operand of the second product, so
 // the hidden never goes through LDS or HBM. W0/W2 slices are double-buffered in LDS.
 // ---------------------------------------------------------------------------
-template <int T, int MT, int HC, bool H16>
-__global__ __launch_bounds__(256) void k_mlp(MlpArgs a) {
+template <int T, int MT, int HC, bool H16, int NWV = 4>
+__global__ __launch_bounds__(NWV * 64) void k_mlp(MlpArgs a) {
+    constexpr int NTH = NWV * 64;
     constexpr int KG = T / 16, NT = T / 16, HT = HC / 16, NCH = 4 * T / HC;
     // Slice pitches: fp32 T + 8 / HC + 8 floats; fp16 T + 16 / HC + 16 halves (2 mod 4
     // sixteen-byte slots either way: conflict-free 128-bit operand reads).
@@ -1010,15 +1011,15 @@ __global__ __launch_bounds__(256) void k_mlp(MlpArgs a) {
     constexpr int BUF = HC * L0 + T * L2;
     constexpr int EV = H16 ? 8 : 4;               // elements per 16-byte chunk
     constexpr int W0V = HC * T / EV;              // chunks in a W0 slice (and in a W2 slice)
-    constexpr int PV = (2 * W0V) / 256;           // chunks per thread per slice (W0 then W2)
-    static_assert((2 * W0V) % 256 == 0 && W0V % 256 == 0, "slice must split evenly");
+    constexpr int PV = (2 * W0V) / NTH;           // chunks per thread per slice (W0 then W2)
+    static_assert((2 * W0V) % NTH == 0 && W0V % NTH == 0, "slice must split evenly");
     static_assert(!H16 || HC % 32 == 0, "fp16 slices are whole 32-wide k blocks");
     using ET = std::conditional_t<H16, _Float16, float>;
     __shared__ __align__(16) ET lds[2 * BUF];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int li = lane & 15, lg = lane >> 4;
-    const long row0 = long(blockIdx.x) * (64 * MT) + wave * 16 * MT;
+    const long row0 = long(blockIdx.x) * (16 * MT * NWV) + wave * 16 * MT;
 
     f4 xa[MT][KG];
 #pragma unroll
@@ -1028,12 +1029,16 @@ __global__ __launch_bounds__(256) void k_mlp(MlpArgs a) {
         for (int kg = 0; kg < KG; ++kg)
             xa[mt][kg] = r < a.M ? ld4(a.x + r * a.ldx + kg * 16 + lg * 4) : f4{0.f, 0.f, 0.f, 0.f};
     }
-    // The raw rows stay in registers for the residual.
-    f4 xr[MT][KG];
+    // The raw rows stay in registers for the residual, unless they would crowd out the
+    // accumulators (then they are read again, from L2, at the end).
+    constexpr bool KEEPX = MT * KG <= 16;
+    f4 xr[KEEPX ? MT : 1][KEEPX ? KG : 1];
+    if constexpr (KEEPX) {
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
+        for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-        for (int kg = 0; kg < KG; ++kg) xr[mt][kg] = xa[mt][kg];
+            for (int kg = 0; kg < KG; ++kg) xr[mt][kg] = xa[mt][kg];
+    }
     // LayerNorm, two-pass (cpu.rs:338-357).
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
@@ -1074,7 +1079,7 @@ __global__ __launch_bounds__(256) void k_mlp(MlpArgs a) {
     auto gload = [&](int ch) {
 #pragma unroll
         for (int i = 0; i < PV; ++i) {
-            const int f = tid + i * 256;
+            const int f = tid + i * NTH;
             if (f < W0V) {
                 const int row = f / (T / EV), c = f % (T / EV);
                 pre[i] = H16 ? ld4(reinterpret_cast<const float*>(a.h0 + long(ch * HC + row) * T + c * 8))
@@ -1091,7 +1096,7 @@ __global__ __launch_bounds__(256) void k_mlp(MlpArgs a) {
         ET* base = lds + b * BUF;
 #pragma unroll
         for (int i = 0; i < PV; ++i) {
-            const int f = tid + i * 256;
+            const int f = tid + i * NTH;
             if (f < W0V) {
                 const int row = f / (T / EV), c = f % (T / EV);
                 st4(reinterpret_cast<float*>(base + row * L0 + c * EV), pre[i]);
@@ -1184,7 +1189,8 @@ __global__ __launch_bounds__(256) void k_mlp(MlpArgs a) {
         for (int mt = 0; mt < MT; ++mt) {
             const long row = row0 + mt * 16 + li;
             if (row < a.M) {
-                st4(a.x + row * a.ldx + nt * 16 + lg * 4, xr[mt][nt] + (acc2[mt][nt] + bv));
+                float* o = a.x + row * a.ldx + nt * 16 + lg * 4;
+                st4(o, (KEEPX ? xr[KEEPX ? mt : 0][KEEPX ? nt : 0] : ld4(o)) + (acc2[mt][nt] + bv));
             }
         }
     }
@@ -1192,9 +1198,9 @@ __global__ __launch_bounds__(256) void k_mlp(MlpArgs a) {
 
 bool mlp(const MlpArgs& a, hipStream_t s, const char** why) {
     if (a.M <= 0) return true;
-    auto go = [&](auto kern, int rows_per_block) {
+    auto go = [&](auto kern, int rows_per_block, int threads = 256) {
         dim3 grid{unsigned((a.M + rows_per_block - 1) / rows_per_block), 1u, 1u};
-        dim3 block{256u, 1u, 1u};
+        dim3 block{unsigned(threads), 1u, 1u};
         hipLaunchKernelGGL(kern, grid, block, 0, s, a);
     };
     if (a.h0 && !a.h2) {
@@ -1205,8 +1211,10 @@ bool mlp(const MlpArgs& a, hipStream_t s, const char** why) {
     switch (a.t) {
         case 32: h16 ? go(k_mlp<32, 4, 64, true>, 256) : go(k_mlp<32, 4, 64, false>, 256); break;
         case 64: h16 ? go(k_mlp<64, 2, 64, true>, 128) : go(k_mlp<64, 2, 64, false>, 128); break;
-        case 128: h16 ? go(k_mlp<128, 1, 32, true>, 64) : go(k_mlp<128, 1, 32, false>, 64); break;
-        case 256: h16 ? go(k_mlp<256, 1, 32, true>, 64) : go(k_mlp<256, 1, 16, false>, 64); break;
+        // fp16: more rows per workgroup (8 waves at t = 128, 2 row tiles per wave at both), so
+        // each streamed weight slice feeds 256 (t = 128) or 128 (t = 256) rows.
+        case 128: h16 ? go(k_mlp<128, 2, 32, true, 8>, 256, 512) : go(k_mlp<128, 1, 32, false>, 64); break;
+        case 256: h16 ? go(k_mlp<256, 2, 32, true>, 128) : go(k_mlp<256, 1, 16, false>, 64); break;
         default: *why = "mlp: t must be 32, 64, 128 or 256"; return false;
     }
     return true;
