@@ -85,6 +85,23 @@ int scunet_hip_forward_dump(scunet_hip* h, const float* x, size_t c, size_t hp, 
 int scunet_hip_run(scunet_hip* h, const float* x, size_t c, size_t hh, size_t ww, float* y);
 int scunet_hip_run_device(scunet_hip* h, const float* x, size_t c, size_t hh, size_t ww, float* y);
 
+/* n images of one size, [n][c][hh][ww] in and out, host buffers: one upload, the n
+ * forwards back to back on the handle's stream, one download (backend::run, backend.rs:63-105,
+ * for a batch of small images without a host round trip per image). */
+int scunet_hip_run_batch(scunet_hip* h, const float* x, size_t n, size_t c, size_t hh, size_t ww, float* y);
+
+/* --- will it fit (src/memguard.rs:66-74 device_need; 1-80 for the policy) ---
+ * The device memory a forward of an hh x ww image (padded to ceil64 on each axis) takes,
+ * computed from the scratch roles the forward requests rather than fitted:
+ * *scratch_bytes = the handle's scratch arena after such a forward (the arena keeps each
+ * role's largest size), *more_bytes = what it does not hold yet. host_io != 0 counts the
+ * host entry points' staging copies of x and y. Weights are not included (footprint).
+ * Every forward entry point asks this before its first allocation and, when *more_bytes
+ * exceeds the device's free memory, fails with a message naming the sizes instead of
+ * failing in an allocation. */
+int scunet_hip_device_need(const scunet_hip* h, size_t c, size_t hh, size_t ww, int host_io,
+                           size_t* scratch_bytes, size_t* more_bytes);
+
 /* --- Backend's bookkeeping (src/backend.rs:30-55) --- */
 int scunet_hip_footprint(const scunet_hip* h, size_t* weight_bytes, size_t* scratch_bytes);
 int scunet_hip_release_scratch(scunet_hip* h);

@@ -650,6 +650,67 @@ bool to_host(scunet_hip* h, float* dst, const float* src, size_t n) {
     return ck(h, hipStreamSynchronize(h->stream), "sync");
 }
 
+// The scratch a forward of the padded H x W plane requests, role by role, exactly as walk()
+// and block() ask buf() for it: the four level planes and three skips (dim 2^k channels at
+// P / 4^k pixels), one ConvTransBlock scratch sized for level 0 (7 t floats per pixel), the
+// stage-dump staging plane when a hook is given, and the host entry points' input/output
+// staging copies (io floats each).
+std::vector<std::pair<std::string, size_t>> arena_plan(const scunet_hip* h, size_t H, size_t W, size_t io,
+                                                       bool dump) {
+    const size_t dim = size_t(h->wt.dim);
+    std::vector<std::pair<std::string, size_t>> r;
+    size_t block = 0;
+    for (int k = 0; k < 4; ++k) {
+        const size_t P = (H >> k) * (W >> k), c = dim << k;
+        r.push_back({"cur" + std::to_string(k), P * c});
+        if (k > 0) r.push_back({"skip" + std::to_string(k), P * c});
+        block = std::max(block, P * 7 * (c / 2));
+    }
+    r.push_back({"block", block});
+    if (dump) r.push_back({"dump", H * W * dim});
+    if (io) {
+        r.push_back({"io_x", io});
+        r.push_back({"io_y", io});
+    }
+    return r;
+}
+
+// (bytes the arena holds for that plan, bytes not held yet). The arena keeps each role's
+// largest size, so a role already big enough costs nothing.
+std::pair<size_t, size_t> arena_need(const scunet_hip* h, const std::vector<std::pair<std::string, size_t>>& plan) {
+    size_t total = 0, more = 0;
+    for (auto& r : plan) {
+        const size_t bytes = std::max<size_t>(r.second, 1) * sizeof(float);
+        auto it = h->arena.find(r.first);
+        const size_t held = it == h->arena.end() ? 0 : it->second.second;
+        total += std::max(bytes, held);
+        // A grown role frees its old buffer just before allocating the new one, so the roles'
+        // growths add up: their sum is both the extra footprint and the peak extra demand.
+        if (bytes > held) more += bytes - held;
+    }
+    for (auto& kv : h->arena) {
+        bool planned = false;
+        for (auto& r : plan) planned = planned || r.first == kv.first;
+        if (!planned) total += kv.second.second;
+    }
+    return {total, more};
+}
+
+// The memguard.rs:66-74 question, asked before the first allocation of a forward: does the
+// scratch it still needs fit in the device's free memory? Refuses with the sizes named.
+bool preflight(scunet_hip* h, size_t H, size_t W, size_t io, bool dump) {
+    const auto need = arena_need(h, arena_plan(h, H, W, io, dump));
+    if (need.second == 0) return true;
+    size_t free_b = 0, total_b = 0;
+    if (!ck(h, hipMemGetInfo(&free_b, &total_b), "hipMemGetInfo")) return false;
+    if (need.second <= free_b) return true;
+    return fail(h, "a " + std::to_string(H) + "x" + std::to_string(W) + " forward needs " +
+                       std::to_string(need.second >> 20) + " MiB more device memory (" +
+                       std::to_string(need.first >> 20) + " MiB of scratch in all, plus " +
+                       std::to_string((h->wbytes + h->h16bytes) >> 20) + " MiB of weights); the device has " +
+                       std::to_string(free_b >> 20) + " MiB free of " + std::to_string(total_b >> 20) + " MiB");
+}
+
 bool shape_ok(scunet_hip* h, size_t c, size_t hp, size_t wp) {
     if (c != size_t(h->wt.in_nc))
         return fail(h, "expected " + std::to_string(h->wt.in_nc) + " channels, got " + std::to_string(c));
@@ -743,6 +804,7 @@ int scunet_hip_arch(const scunet_hip* h, int* in_nc, int* dim, int* head_dim, in
 int scunet_hip_forward_device(scunet_hip* h, const float* x, size_t c, size_t hp, size_t wp, float* y) {
     return guard(h, [&] {
         if (!shape_ok(h, c, hp, wp)) return false;
+        if (!preflight(h, hp, wp, 0, false)) return false;
         return walk(h, x, int(hp), int(wp), int(hp), int(wp), y, int(hp), int(wp), nullptr, nullptr);
     });
 }
@@ -752,6 +814,7 @@ int scunet_hip_forward_dump(scunet_hip* h, const float* x, size_t c, size_t hp, 
     return guard(h, [&] {
         if (!shape_ok(h, c, hp, wp)) return false;
         size_t n = c * hp * wp;
+        if (!preflight(h, hp, wp, n, hook != nullptr)) return false;
         float *dx, *dy;
         if (!to_device(h, "io_x", x, n, &dx)) return false;
         dy = buf(h, "io_y", n);
@@ -771,6 +834,7 @@ int scunet_hip_run_device(scunet_hip* h, const float* x, size_t c, size_t hh, si
         if (c != size_t(h->wt.in_nc))
             return fail(h, "expected " + std::to_string(h->wt.in_nc) + " channels, got " + std::to_string(c));
         size_t hp = pad64(hh), wp = pad64(ww);
+        if (!preflight(h, hp, wp, 0, false)) return false;
         return walk(h, x, int(hh), int(ww), int(hp), int(wp), y, int(hh), int(ww), nullptr, nullptr);
     });
 }
@@ -781,6 +845,7 @@ int scunet_hip_run(scunet_hip* h, const float* x, size_t c, size_t hh, size_t ww
         if (c != size_t(h->wt.in_nc))
             return fail(h, "expected " + std::to_string(h->wt.in_nc) + " channels, got " + std::to_string(c));
         size_t hp = pad64(hh), wp = pad64(ww), n = c * hh * ww;
+        if (!preflight(h, hp, wp, n, false)) return false;
         float *dx, *dy;
         if (!to_device(h, "io_x", x, n, &dx)) return false;
         dy = buf(h, "io_y", n);
@@ -788,6 +853,34 @@ int scunet_hip_run(scunet_hip* h, const float* x, size_t c, size_t hh, size_t ww
         if (!walk(h, dx, int(hh), int(ww), int(hp), int(wp), dy, int(hh), int(ww), nullptr, nullptr)) return false;
         return to_host(h, y, dy, n);
     });
+}
+
+int scunet_hip_run_batch(scunet_hip* h, const float* x, size_t nimg, size_t c, size_t hh, size_t ww, float* y) {
+    return guard(h, [&] {
+        if (!check_min_size(h, hh, ww)) return false;
+        if (c != size_t(h->wt.in_nc))
+            return fail(h, "expected " + std::to_string(h->wt.in_nc) + " channels, got " + std::to_string(c));
+        if (nimg == 0) return true;
+        size_t hp = pad64(hh), wp = pad64(ww), n = c * hh * ww;
+        if (!preflight(h, hp, wp, n * nimg, false)) return false;
+        float *dx, *dy;
+        if (!to_device(h, "io_x", x, n * nimg, &dx)) return false;
+        dy = buf(h, "io_y", n * nimg);
+        if (!dy) return false;
+        for (size_t i = 0; i < nimg; ++i)
+            if (!walk(h, dx + i * n, int(hh), int(ww), int(hp), int(wp), dy + i * n, int(hh), int(ww), nullptr, nullptr))
+                return false;
+        return to_host(h, y, dy, n * nimg);
+    });
+}
+
+int scunet_hip_device_need(const scunet_hip* h, size_t c, size_t hh, size_t ww, int host_io, size_t* scratch_bytes,
+                           size_t* more_bytes) {
+    if (!h || hh == 0 || ww == 0) return 1;
+    const auto need = arena_need(h, arena_plan(h, pad64(hh), pad64(ww), host_io ? c * hh * ww : 0, false));
+    if (scratch_bytes) *scratch_bytes = need.first;
+    if (more_bytes) *more_bytes = need.second;
+    return 0;
 }
 
 int scunet_hip_footprint(const scunet_hip* h, size_t* weight_bytes, size_t* scratch_bytes) {

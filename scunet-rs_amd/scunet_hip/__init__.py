@@ -25,7 +25,8 @@ EXPORTS = [
     "scunet_hip_create", "scunet_hip_create_error", "scunet_hip_destroy", "scunet_hip_last_error",
     "scunet_hip_name", "scunet_hip_arch", "scunet_hip_set_precision", "scunet_hip_precision",
     "scunet_hip_forward", "scunet_hip_forward_device",
-    "scunet_hip_forward_dump", "scunet_hip_run", "scunet_hip_run_device", "scunet_hip_footprint",
+    "scunet_hip_forward_dump", "scunet_hip_run", "scunet_hip_run_device", "scunet_hip_run_batch",
+    "scunet_hip_device_need", "scunet_hip_footprint",
     "scunet_hip_release_scratch", "scunet_hip_synchronize", "scunet_hip_stream", "scunet_hip_profile",
     "scunet_hip_profile_report", "scunet_hip_malloc", "scunet_hip_free", "scunet_hip_h2d", "scunet_hip_d2h",
     "scunet_hip_copy",
@@ -72,6 +73,8 @@ def load_library(path=None):
     L.scunet_hip_forward_dump.argtypes = [_vp, _f, _sz, _sz, _sz, _f, HOOK, _vp]
     L.scunet_hip_run.argtypes = [_vp, _f, _sz, _sz, _sz, _f]
     L.scunet_hip_run_device.argtypes = [_vp, _vp, _sz, _sz, _sz, _vp]
+    L.scunet_hip_run_batch.argtypes = [_vp, _f, _sz, _sz, _sz, _sz, _f]
+    L.scunet_hip_device_need.argtypes = [_vp, _sz, _sz, _sz, ctypes.c_int, ctypes.POINTER(_sz), ctypes.POINTER(_sz)]
     L.scunet_hip_footprint.argtypes = [_vp, ctypes.POINTER(_sz), ctypes.POINTER(_sz)]
     L.scunet_hip_release_scratch.argtypes = [_vp]
     L.scunet_hip_synchronize.argtypes = [_vp]
@@ -305,6 +308,21 @@ class Hip:
         y = np.empty_like(x)
         self._check(self._lib.scunet_hip_run(self._h, _p(x), c, h, w, _p(y)))
         return y
+
+    def run_batch(self, x):
+        """n images of one size, [n][c][h][w]: one upload, n forwards, one download."""
+        x = _c32(x)
+        n, c, h, w = x.shape
+        y = np.empty_like(x)
+        self._check(self._lib.scunet_hip_run_batch(self._h, _p(x), n, c, h, w, _p(y)))
+        return y
+
+    def device_need(self, h, w, host_io=True):
+        """(scratch bytes after an h x w forward, bytes not held yet): memguard's device_need."""
+        tot, more = _sz(), _sz()
+        self._check(self._lib.scunet_hip_device_need(self._h, self.in_nc, h, w, int(host_io),
+                                                     ctypes.byref(tot), ctypes.byref(more)))
+        return tot.value, more.value
 
     # -- probes (cuda.rs:1153-1597) --
     def block_dump(self, prefix, h, w, shift, x):

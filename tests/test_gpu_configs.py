@@ -285,3 +285,46 @@ def test_persistent_and_tiled_gemm_agree(weights_path, owt):
     finally:
         pers.close()
         tiled.close()
+
+
+def test_device_need_is_exact_and_refuses_before_allocating(weights_path):
+    """memguard.rs:66-74's device_need, computed from the forward's scratch roles: after a
+    forward the arena is exactly the predicted size and nothing more is needed for that
+    size; a size that cannot fit is refused with the sizes named before anything is
+    allocated or launched (the input buffer here is far smaller than the claimed size: no
+    kernel may read it)."""
+    from scunet_hip import BackendError, Hip, synth
+    with Hip(weights_path) as be:
+        tot, more = be.device_need(80, 72)
+        assert more == tot > 0
+        x = synth.noisy_image(3, 3, 80, 72, 25)
+        be.run_fused(x)
+        assert be.footprint()[1] == tot
+        assert be.device_need(80, 72) == (tot, 0)
+        assert be.device_need(64, 64)[1] == 0
+        tot2, more2 = be.device_need(256, 192)
+        assert tot2 > tot and more2 == tot2 - tot
+        be.run_fused(synth.noisy_image(4, 3, 256, 192, 25))
+        assert be.footprint()[1] == tot2
+        # 1600 bytes of scratch per padded pixel: 120 + 56 + 224 floats (planes, skips, block).
+        t3, _ = be.device_need(1024, 1024, host_io=False)
+        assert t3 >= 1600 * 1024 * 1024
+        before = be.footprint()
+        xp = be.malloc(1 << 20)
+        yp = be.malloc(1 << 20)
+        try:
+            with pytest.raises(BackendError, match=r"a 131072x131072 forward needs \d+ MiB more device memory"):
+                be.run_device(xp, 3, 131072, 131072, yp)
+        finally:
+            be.free(xp)
+            be.free(yp)
+        assert be.footprint() == before
+
+
+def test_run_batch_equals_single_runs(weights_path):
+    from scunet_hip import Hip, synth
+    xs = np.stack([synth.noisy_image(10 + i, 3, 72, 80, 25) for i in range(3)])
+    with Hip(weights_path) as be:
+        ys = be.run_batch(xs)
+        for i in range(3):
+            assert np.array_equal(ys[i], be.run_fused(xs[i])), i
