@@ -131,6 +131,7 @@ def main():
                     help="time the steps without the per-launch event pairs")
     ap.add_argument("--no-attn-sweep", action="store_true", help="skip the config-5 attention sweep")
     ap.add_argument("--no-fp16", action="store_true", help="skip the fp16-operand mode's line")
+    ap.add_argument("--profile-fp16", action="store_true", help="with --profile-pass: the forward in the fp16 mode")
     ap.add_argument("--profile-pass", action="store_true",
                     help="for rocprofv3 counter runs: one forward plus one 256 MiB device copy (the "
                          "calibration kernel), nothing else; prints no JSON line")
@@ -156,6 +157,10 @@ def main():
         f"warmup {args.warmup}, steps {args.steps}")
 
     if args.profile_pass:
+        if args.profile_fp16:
+            be.set_precision("fp16")
+            be.run_device(xp, c, h, w, yp)      # the fp16 weight copies are built before the pass
+            be.synchronize()
         nbytes = 256 << 20
         a_, b_ = be.malloc(nbytes), be.malloc(nbytes)
         be.copy(b_, a_, nbytes)
