@@ -328,3 +328,34 @@ def test_run_batch_equals_single_runs(weights_path):
         ys = be.run_batch(xs)
         for i in range(3):
             assert np.array_equal(ys[i], be.run_fused(xs[i])), i
+
+
+def test_config4_gray_4096_full_size(weights_path_gray):
+    """BASELINE config 4 at its real size, 1x1x4096x4096 (the size whose unfused hidden
+    layer passes 2^31 elements): the whole forward is finite, bit-identical on repeat, and the
+    device pad/crop path equals the plain forward (4096 needs no padding). One level-0
+    ConvTransBlock over the full 4096^2 plane (64 channels, both window phases) is checked
+    against the oracle on a middle band: the block is local (two 3x3 convolutions, 8x8
+    windows aligned to the plane, the cyclic roll and its mask acting only at the plane's
+    edges), so output rows 16 or more away from the band's cut see exactly what they see in
+    the full plane."""
+    from scunet_hip import Hip, Plan, synth
+    owt = O.Weights.load(weights_path_gray)
+    x = synth.config_input(4)
+    assert x.shape == (1, 4096, 4096)
+    with Hip(weights_path_gray) as be:
+        a = be.run_fused(x)
+        assert np.isfinite(a).all()
+        assert np.array_equal(a, be.run_fused(x))
+        assert np.array_equal(a, be.forward(x, Plan(4096, 4096)))
+        assert 0.0 < float(np.abs(a).mean()) < 10.0
+        c = sum(owt.block_dims("m_down1.1"))
+        rng = np.random.default_rng(44)
+        xb = rng.standard_normal((c, 4096, 4096), dtype=np.float32)
+        r0, r1, m = 1984, 2112, 16
+        for shift in (0, 4):
+            got = be.block_dump("m_down1.1", 4096, 4096, shift, xb)
+            band = np.ascontiguousarray(xb[:, r0 - m:r1 + m])
+            want = O.conv_trans_block(owt, "m_down1.1", band, shift)[:, m:-m]
+            assert max_abs(want, got[:, r0:r1]) <= STAGE_TOL, shift
+            assert np.isfinite(got).all()
