@@ -678,7 +678,10 @@ static void launch_gemm3_h16(const GemmArgs& g, GemmA a, GemmE e, hipStream_t s)
 
 static bool launch_gemm3(const GemmArgs& g, GemmA a, GemmE e, hipStream_t s) {
     if (g.W16 && a != A_LN && g.K % 32 == 0 && g.N % 64 == 0) {
-        if (g.N <= 128) launch_gemm3_h16<2, 64>(g, a, e, s);
+        // The level-0 down-conv (N = 128) reads its patches once with a 128-wide N block:
+        // 382 -> 268 us per launch; the other shapes measured best as below.
+        if (a == A_S2D && g.N == 128) launch_gemm3_h16<1, 128>(g, a, e, s);
+        else if (g.N <= 128) launch_gemm3_h16<2, 64>(g, a, e, s);
         else if (g.N % 128 == 0) launch_gemm3_h16<2, 128>(g, a, e, s);
         else launch_gemm3_h16<4, 64>(g, a, e, s);
         return true;
@@ -686,7 +689,12 @@ static bool launch_gemm3(const GemmArgs& g, GemmA a, GemmE e, hipStream_t s) {
     // The LayerNorm operand keeps its row in registers (k_gemm2); the skip-sum operand with
     // the depth-to-space epilogue measured faster one tile per workgroup (k_gemm2).
     if (a == A_LN || a == A_ADD2) return false;
-    if (g.N % 64 == 0 && g.N <= 128) launch_gemm3_a<2, 64, 32>(g, a, e, s);
+    // Measured on the 1080p forward: one 16-row tile per wave and a wide N block for the 1x1
+    // at 256 and 512 channels (4-6 % faster than two tiles per wave) and for the level-0
+    // down-conv (N = 128: 9 %); the other down-convs keep two tiles per wave.
+    if (a == A_ROWS && g.N >= 512 && g.N % 256 == 0) launch_gemm3_a<1, 256, 32>(g, a, e, s);
+    else if ((a == A_ROWS && g.N == 256) || (a == A_S2D && g.N == 128)) launch_gemm3_a<1, 128, 32>(g, a, e, s);
+    else if (g.N % 64 == 0 && g.N <= 128) launch_gemm3_a<2, 64, 32>(g, a, e, s);
     else if (g.N % 128 == 0) launch_gemm3_a<2, 128, 32>(g, a, e, s);
     else if (g.N % 96 == 0) launch_gemm3_a<2, 96, 32>(g, a, e, s);
     else if (g.N % 64 == 0) launch_gemm3_a<4, 64, 32>(g, a, e, s);
