@@ -116,7 +116,7 @@ struct Conv3Args {
     float* out = nullptr;
     long ldo = 0;
     int H = 0, W = 0, cin = 0, cout = 0;
-    int cblock = 0;                // Winograd: output channels per unit (0 = 32 when possible, 16)
+    int cblock = 0;                // Winograd: output channels per unit (0 = 32 below 256 input channels, else 16; 16)
     const half_t* w16 = nullptr;   // fp16 mode: [9][cout][cin] k-permuted (conv3x3_h16)
 };
 // relu=true: out = relu(conv); relu=false: out += conv (the conv half's residual).

@@ -1810,7 +1810,9 @@ bool conv3x3_winograd(const Conv3Args& a, bool relu, hipStream_t s, const char**
         *why = "conv3x3_winograd: plane too large for 32-bit element offsets";
         return false;
     }
-    const bool wide = a.cout % 32 == 0 && a.cin >= 32 && a.cblock != 16;
+    // 32 output channels per unit, except at cin >= 256 (level 3 of the forward), where the
+    // 16-channel kernel measured faster (238 against 247 us per launch at 1080p).
+    const bool wide = a.cout % 32 == 0 && a.cin >= 32 && a.cin < 256 && a.cblock != 16;
     const bool ures = wide && a.cin == 32 && a.cout == 32;
     static int per_cu[6] = {-1, -1, -1, -1, -1, -1}, cus = 0;
     int& pc = per_cu[(relu ? 1 : 0) + (ures ? 4 : wide ? 2 : 0)];
