@@ -318,7 +318,7 @@ __global__ __launch_bounds__(256) void k_gemm2(GemmArgs g) {
             }
             q += __shfl_xor(q, 16);
             q += __shfl_xor(q, 32);
-            const float rs = 1.0f / sqrtf(q / float(KLN) + 1e-5f);
+            const float rs = __builtin_amdgcn_rsqf(q * (1.0f / float(KLN)) + 1e-5f);
 #pragma unroll
             for (int kg = 0; kg < XKG; ++kg) {
                 f4 gg = ld4(g.ln_g + kg * 16 + lg * 4), bb = ld4(g.ln_b + kg * 16 + lg * 4);
@@ -1072,7 +1072,7 @@ __global__ __launch_bounds__(NWV * 64) void k_mlp(MlpArgs a) {
         }
         q += __shfl_xor(q, 16);
         q += __shfl_xor(q, 32);
-        const float rs = 1.0f / sqrtf(q / float(T) + 1e-5f);
+        const float rs = __builtin_amdgcn_rsqf(q * (1.0f / float(T)) + 1e-5f);
 #pragma unroll
         for (int kg = 0; kg < KG; ++kg) {
             f4 g = ld4(a.ln_g + kg * 16 + lg * 4), b = ld4(a.ln_b + kg * 16 + lg * 4);
@@ -2263,7 +2263,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(T == 32 ? 2
             }
             q += __shfl_xor(q, 16);
             q += __shfl_xor(q, 32);
-            const float rs = 1.0f / sqrtf(q / float(T) + 1e-5f);
+            const float rs = __builtin_amdgcn_rsqf(q * (1.0f / float(T)) + 1e-5f);
 #pragma unroll
             for (int kg = 0; kg < KG; ++kg) {
                 f4 gg = ld4(a.ln_g + kg * 16 + lg * 4), bb = ld4(a.ln_b + kg * 16 + lg * 4);
@@ -2285,6 +2285,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(T == 32 ? 2
     const bool row_edge = a.shift > 0 && wh == a.nwh - 1;
     const bool col_edge = a.shift > 0 && ww == a.nww - 1;
     const float SENT = -3.4028234663852886e38f / 4.0f;
+    const float sc2 = a.scale * 1.4426950408889634f;   // logits in log2 units: p = 2^(l - max)
     f4 acc[4][OT];
 #pragma unroll
     for (int nt = 0; nt < 4; ++nt)
@@ -2400,7 +2401,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(T == 32 ? 2
                 const bool hit = (row_edge && (q_row_lo != (mt < 2))) || (col_edge && (q_col_lo != k_col_lo));
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    float v = S[mt][r] * a.scale + b[r];
+                    float v = fmaf(S[mt][r], sc2, b[r]);
                     if (hit) v = SENT;
                     S[mt][r] = v;
                     mx = fmaxf(mx, v);
@@ -2413,21 +2414,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(T == 32 ? 2
             for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    const float e = __expf(S[mt][r] - mx);
+                    const float e = __builtin_amdgcn_exp2f(S[mt][r] - mx);
                     S[mt][r] = e;
                     sum += e;
                 }
             sum += __shfl_xor(sum, 16);
             sum += __shfl_xor(sum, 32);
-            const float inv = 1.0f / sum;
+            const float inv = __builtin_amdgcn_rcpf(sum);
             f4 O[2] = {f4{0.f, 0.f, 0.f, 0.f}, f4{0.f, 0.f, 0.f, 0.f}};
             if constexpr (H16) {
 #pragma unroll
                 for (int kk = 0; kk < 2; ++kk) {
-                    const h8 ph = pack8(S[2 * kk] * inv, S[2 * kk + 1] * inv);
+                    const h8 ph = pack8(S[2 * kk], S[2 * kk + 1]);
 #pragma unroll
                     for (int nd = 0; nd < 2; ++nd) O[nd] = mfma16(vh[kk][nd], ph, O[nd]);
                 }
+                O[0] = O[0] * inv;
+                O[1] = O[1] * inv;
                 // out^T += Wp[:, head dims] O^T: the head's dims are k block h of Wp.
                 const h8 oh = pack8(O[0], O[1]);
 #pragma unroll
@@ -2438,10 +2441,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(T == 32 ? 2
                 for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
-                        const float p = S[kt][r] * inv;
 #pragma unroll
-                        for (int nd = 0; nd < 2; ++nd) O[nd] = mfma4(vf[kt][nd][r], p, O[nd]);
+                        for (int nd = 0; nd < 2; ++nd) O[nd] = mfma4(vf[kt][nd][r], S[kt][r], O[nd]);
                     }
+                O[0] = O[0] * inv;
+                O[1] = O[1] * inv;
                 // out^T += Wp[:, head dims] O^T.
 #pragma unroll
                 for (int ot = 0; ot < OT; ++ot)
@@ -2485,7 +2489,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(T == 32 ? 2
             }
             q += __shfl_xor(q, 16);
             q += __shfl_xor(q, 32);
-            const float rs = 1.0f / sqrtf(q / float(T) + 1e-5f);
+            const float rs = __builtin_amdgcn_rsqf(q * (1.0f / float(T)) + 1e-5f);
 #pragma unroll
             for (int kg = 0; kg < OT; ++kg) {
                 f4 gg = ld4(a.ln2_g + kg * 16 + lg * 4), bb = ld4(a.ln2_b + kg * 16 + lg * 4);
@@ -2637,7 +2641,7 @@ __global__ __launch_bounds__(T * 2) __attribute__((amdgpu_waves_per_eu(2, 2))) v
         }
         q += __shfl_xor(q, 16);
         q += __shfl_xor(q, 32);
-        const float rs = 1.0f / sqrtf(q / float(T) + 1e-5f);
+        const float rs = __builtin_amdgcn_rsqf(q * (1.0f / float(T)) + 1e-5f);
 #pragma unroll
         for (int kg = 0; kg < KG; ++kg) {
             f4 gg = ld4(a.ln_g + kg * 16 + lg * 4), bb = ld4(a.ln_b + kg * 16 + lg * 4);
@@ -2726,6 +2730,7 @@ __global__ __launch_bounds__(T * 2) __attribute__((amdgpu_waves_per_eu(2, 2))) v
         const bool row_edge = a.shift > 0 && wh == a.nwh - 1;
         const bool col_edge = a.shift > 0 && ww == a.nww - 1;
         const float SENT = -3.4028234663852886e38f / 4.0f;
+        const float sc2 = a.scale * 1.4426950408889634f;   // logits in log2 units: p = 2^(l - max)
         const float* tab = a.tab + (long(h) * 64 + lane) * 64;
         h8 kh[H16 ? 4 : 1], qh[H16 ? 4 : 1], vh[H16 ? 2 : 1][2];
         if constexpr (H16) {
@@ -2765,7 +2770,7 @@ __global__ __launch_bounds__(T * 2) __attribute__((amdgpu_waves_per_eu(2, 2))) v
                 const bool hit = (row_edge && (q_row_lo != (mt < 2))) || (col_edge && (q_col_lo != k_col_lo));
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    float v = S[mt][r] * a.scale + b[r];
+                    float v = fmaf(S[mt][r], sc2, b[r]);
                     if (hit) v = SENT;
                     S[mt][r] = v;
                     mx = fmaxf(mx, v);
@@ -2778,21 +2783,23 @@ __global__ __launch_bounds__(T * 2) __attribute__((amdgpu_waves_per_eu(2, 2))) v
             for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    const float e = __expf(S[mt][r] - mx);
+                    const float e = __builtin_amdgcn_exp2f(S[mt][r] - mx);
                     S[mt][r] = e;
                     sum += e;
                 }
             sum += __shfl_xor(sum, 16);
             sum += __shfl_xor(sum, 32);
-            const float inv = 1.0f / sum;
+            const float inv = __builtin_amdgcn_rcpf(sum);
             f4 O[2] = {f4{0.f, 0.f, 0.f, 0.f}, f4{0.f, 0.f, 0.f, 0.f}};
             if constexpr (H16) {
 #pragma unroll
                 for (int kk = 0; kk < 2; ++kk) {
-                    const h8 ph = pack8(S[2 * kk] * inv, S[2 * kk + 1] * inv);
+                    const h8 ph = pack8(S[2 * kk], S[2 * kk + 1]);
 #pragma unroll
                     for (int nd = 0; nd < 2; ++nd) O[nd] = mfma16(vh[kk][nd], ph, O[nd]);
                 }
+                O[0] = O[0] * inv;
+                O[1] = O[1] * inv;
                 // The head's dims are k block h of the projection.
                 sth8(osh + (nt * 16 + li) * PH + h * 32 + lg * 8, pack8(O[0], O[1]));
             } else {
@@ -2800,10 +2807,11 @@ __global__ __launch_bounds__(T * 2) __attribute__((amdgpu_waves_per_eu(2, 2))) v
                 for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
-                        const float p = S[kt][r] * inv;
 #pragma unroll
-                        for (int nd = 0; nd < 2; ++nd) O[nd] = mfma4(vf[kt][nd][r], p, O[nd]);
+                        for (int nd = 0; nd < 2; ++nd) O[nd] = mfma4(vf[kt][nd][r], S[kt][r], O[nd]);
                     }
+                O[0] = O[0] * inv;
+                O[1] = O[1] * inv;
                 // Lanes hold dims 16nd + 4lg .. +3 of query 16nt + li.
 #pragma unroll
                 for (int nd = 0; nd < 2; ++nd) st4(os + (nt * 16 + li) * LDX + h * 32 + nd * 16 + lg * 4, O[nd]);
@@ -2895,7 +2903,7 @@ __global__ __launch_bounds__(T * 2) __attribute__((amdgpu_waves_per_eu(2, 2))) v
             }
             q += __shfl_xor(q, 16);
             q += __shfl_xor(q, 32);
-            const float rs = 1.0f / sqrtf(q / float(T) + 1e-5f);
+            const float rs = __builtin_amdgcn_rsqf(q * (1.0f / float(T)) + 1e-5f);
 #pragma unroll
             for (int kg = 0; kg < KG; ++kg) {
                 f4 gg = ld4(a.ln2_g + kg * 16 + lg * 4), bb = ld4(a.ln2_b + kg * 16 + lg * 4);
@@ -3017,8 +3025,9 @@ bool msa_fused(const MsaArgs& a, hipStream_t s, const char** why) {
 }
 
 void build_bias_table(const float* rp, int heads, float* tab) {
-    // tab[h][lane][nt][mt][r] = B_h[query 16nt + lane%16][key 16mt + 4(lane/16) + r],
-    // B_h[p][q] = rp[h][(p/8 - q/8 + 7)][(p%8 - q%8 + 7)]   (cpu.rs:532-546).
+    // tab[h][lane][nt][mt][r] = log2(e) B_h[query 16nt + lane%16][key 16mt + 4(lane/16) + r],
+    // B_h[p][q] = rp[h][(p/8 - q/8 + 7)][(p%8 - q%8 + 7)]   (cpu.rs:532-546); the window
+    // kernels keep logits in log2 units (softmax as 2^(l - max)).
     for (int h = 0; h < heads; ++h)
         for (int lane = 0; lane < 64; ++lane)
             for (int nt = 0; nt < 4; ++nt)
@@ -3027,7 +3036,8 @@ void build_bias_table(const float* rp, int heads, float* tab) {
                         int p = nt * 16 + (lane & 15);
                         int q = mt * 16 + (lane >> 4) * 4 + r;
                         int dy = p / 8 - q / 8 + 7, dx = p % 8 - q % 8 + 7;
-                        tab[((long(h) * 64 + lane) * 4 + nt) * 16 + mt * 4 + r] = rp[h * 225 + dy * 15 + dx];
+                        tab[((long(h) * 64 + lane) * 4 + nt) * 16 + mt * 4 + r] =
+                            float(double(rp[h * 225 + dy * 15 + dx]) * 1.4426950408889634);
                     }
 }
 
