@@ -85,9 +85,11 @@ int scunet_hip_forward_dump(scunet_hip* h, const float* x, size_t c, size_t hp, 
 int scunet_hip_run(scunet_hip* h, const float* x, size_t c, size_t hh, size_t ww, float* y);
 int scunet_hip_run_device(scunet_hip* h, const float* x, size_t c, size_t hh, size_t ww, float* y);
 
-/* n images of one size, [n][c][hh][ww] in and out, host buffers: one upload, the n
- * forwards back to back on the handle's stream, one download (backend::run, backend.rs:63-105,
- * for a batch of small images without a host round trip per image). */
+/* n images of one size, [n][c][hh][ww] in and out, host buffers (backend::run,
+ * backend.rs:63-105, over a batch): one upload, one forward over the n padded images stacked
+ * along y as one plane (every kernel keeps each image's edges as plane edges, so each
+ * result is bit-identical to the image's own forward), one download. Many small images then
+ * fill the device as one large one does. */
 int scunet_hip_run_batch(scunet_hip* h, const float* x, size_t n, size_t c, size_t hh, size_t ww, float* y);
 
 /* --- will it fit (src/memguard.rs:66-74 device_need; 1-80 for the policy) ---

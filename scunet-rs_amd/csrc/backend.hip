@@ -402,11 +402,12 @@ bool run_pconv(scunet_hip* h, const PconvArgs& a, PconvMode mode) {
 // output into the block scratch. next: the following block of the same stage, whose
 // conv1_1 is then chained onto this block's conv1_2 (empty for the last block).
 bool block(scunet_hip* h, const std::string& p, float* x, int H, int Wd, int shift, bool y_ready = false,
-           const std::string& next = std::string()) {
+           const std::string& next = std::string(), int nimg = 1) {
     auto dims = h->wt.block_dims(p);
     const int t = dims.second, conv = dims.first, c = conv + t;
     if (conv != t) return fail(h, p + ": conv and trans halves of different widths are not supported");
-    const long P = long(H) * Wd;
+    // nimg images of H x Wd stacked along y: the per-pixel work sees one plane of P pixels.
+    const long P = long(H) * Wd * nimg;
     BlockScratch s;
     if (!block_scratch(h, P, t, &s)) return false;
     const std::string tp = p + ".trans_block";
@@ -427,7 +428,7 @@ bool block(scunet_hip* h, const std::string& p, float* x, int H, int Wd, int shi
     // conv half: s1 = relu(conv3x3(y[:, :t])); y[:, :t] += conv3x3(s1).
     Conv3Args cv;
     cv.in = s.y; cv.ldi = c; cv.out = s.s1; cv.ldo = t;
-    cv.H = H; cv.W = Wd; cv.cin = t; cv.cout = t;
+    cv.H = H * nimg; cv.W = Wd; cv.cin = t; cv.cout = t; cv.img_h = nimg > 1 ? H : 0;
     if (!run_conv3(h, p + ".conv_block.0", cv, true)) return false;
     cv.in = s.s1; cv.ldi = t; cv.out = s.y; cv.ldo = c;
     if (!run_conv3(h, p + ".conv_block.2", cv, false)) return false;
@@ -442,6 +443,7 @@ bool block(scunet_hip* h, const std::string& p, float* x, int H, int Wd, int shi
         m.wqkv = W(h, tp + ".msa.embedding_layer.weight"); m.bqkv = W(h, tp + ".msa.embedding_layer.bias");
         m.wp = W(h, tp + ".msa.linear.weight"); m.bp = W(h, tp + ".msa.linear.bias"); m.tab = h->tab[p];
         m.t = t; m.nwh = H / 8; m.nww = Wd / 8; m.H = H; m.W = Wd; m.shift = shift; m.scale = h->scale;
+        m.nimg = nimg;
         m.hqkv = W16(h, tp + ".msa.embedding_layer.weight"); m.hp = W16(h, tp + ".msa.linear.weight");
         if (mlp_in_msa) {
             m.ln2_g = W(h, tp + ".ln2.weight"); m.ln2_b = W(h, tp + ".ln2.bias");
@@ -449,7 +451,7 @@ bool block(scunet_hip* h, const std::string& p, float* x, int H, int Wd, int shi
             m.w2 = W(h, tp + ".mlp.2.weight"); m.b2 = W(h, tp + ".mlp.2.bias");
             m.h0 = W16(h, tp + ".mlp.0.weight"); m.h2 = W16(h, tp + ".mlp.2.weight");
         }
-        const double nw = double(m.nwh) * m.nww;
+        const double nw = double(m.nwh) * m.nww * nimg;
         const double msa_flop = 64.0 * nw * (8.0 * t * t) + 16384.0 * t * nw;
         Span sp(h, mlp_in_msa ? "tblock_fused" : "msa_fused", msa_flop + (mlp_in_msa ? mlp_flop : 0.0),
                 4.0 * (2.0 * P * t + 4.0 * t * t + (mlp_in_msa ? 8.0 * t * t : 0.0)));
@@ -489,13 +491,14 @@ bool block(scunet_hip* h, const std::string& p, float* x, int H, int Wd, int shi
 // The `count` blocks `prefix` first .. first+count-1 of one stage, in place on x; block i
 // uses the shifted windows when i is odd (cpu.rs:1216-1222, 1298-1302). With the resident-weight 1x1
 // kernel, each block's conv1_2 is chained with the next block's conv1_1.
-bool stage_blocks(scunet_hip* h, const std::string& prefix, int first, int count, float* x, int H, int Wd) {
+bool stage_blocks(scunet_hip* h, const std::string& prefix, int first, int count, float* x, int H, int Wd,
+                  int nimg = 1) {
     const int win = h->wt.window;
     const int c = h->wt.block_dims(prefix + std::to_string(first)).first * 2;
     const bool chain = pconv_supported(c) && !h->gemm1x1;
     for (int i = 0; i < count; ++i) {
         const std::string next = chain && i + 1 < count ? prefix + std::to_string(first + i + 1) : std::string();
-        if (!block(h, prefix + std::to_string(first + i), x, H, Wd, (i & 1) ? win / 2 : 0, chain && i > 0, next))
+        if (!block(h, prefix + std::to_string(first + i), x, H, Wd, (i & 1) ? win / 2 : 0, chain && i > 0, next, nimg))
             return false;
     }
     return true;
@@ -519,7 +522,7 @@ bool dump_plane(scunet_hip* h, scunet_stage_hook hook, void* user, const char* n
 // The walker. x: NCHW image of size hh x ww (hh == H, ww == W when already padded);
 // y: NCHW [in_nc][oh][ow] (the crop is fused into m_tail).
 bool walk(scunet_hip* h, const float* x, int hh, int ww, int H, int Wd, float* y, int oh, int ow,
-          scunet_stage_hook hook, void* user) {
+          scunet_stage_hook hook, void* user, int nimg = 1) {
     const Weights& wt = h->wt;
     const int dim = wt.dim, in_nc = wt.in_nc;
     if (H % 64 || Wd % 64) return fail(h, "the padded plane must be a multiple of 64 on each axis");
@@ -528,7 +531,7 @@ bool walk(scunet_hip* h, const float* x, int hh, int ww, int H, int Wd, float* y
     for (int k = 0; k < 4; ++k) {
         Hs[k] = H >> k;
         Ws[k] = Wd >> k;
-        P[k] = long(Hs[k]) * Ws[k];
+        P[k] = long(Hs[k]) * Ws[k] * nimg;
     }
     h->chain = nullptr;
     float* cur[4];
@@ -544,7 +547,7 @@ bool walk(scunet_hip* h, const float* x, int hh, int ww, int H, int Wd, float* y
     h->tag.clear();
     {
         Span sp(h, "head", 2.0 * 9 * in_nc * dim * double(P[0]), 4.0 * (in_nc + dim) * double(P[0]));
-        if (!head_conv(x, in_nc, hh, ww, H, Wd, W(h, "m_head.0.weight"), dim, cur[0], false, h->stream))
+        if (!head_conv(x, in_nc, hh, ww, H, Wd, W(h, "m_head.0.weight"), dim, cur[0], false, h->stream, nimg))
             return fail(h, "m_head: unsupported shape");
         if (!launched(h, "m_head")) return false;
     }
@@ -554,7 +557,7 @@ bool walk(scunet_hip* h, const float* x, int hh, int ww, int H, int Wd, float* y
         const int count = wt.config[k];
         const int c = dim << k;
         h->tag = "@L" + std::to_string(k);
-        if (!stage_blocks(h, "m_" + name + ".", 0, count, cur[k], Hs[k], Ws[k])) return false;
+        if (!stage_blocks(h, "m_" + name + ".", 0, count, cur[k], Hs[k], Ws[k], nimg)) return false;
         if (!dump_plane(h, hook, user, ("m_" + name + "_blocks").c_str(), cur[k], c, P[k])) return false;
         GemmArgs g;
         g.A = cur[k]; g.lda = c; g.W = W(h, "m_" + name + "." + std::to_string(count) + ".weight");
@@ -564,7 +567,7 @@ bool walk(scunet_hip* h, const float* x, int hh, int ww, int H, int Wd, float* y
         if (!dump_plane(h, hook, user, ("m_" + name).c_str(), skip[k + 1], 2 * c, P[k + 1])) return false;
     }
     h->tag = "@L3";
-    if (!stage_blocks(h, "m_body.", 0, wt.config[3], cur[3], Hs[3], Ws[3])) return false;
+    if (!stage_blocks(h, "m_body.", 0, wt.config[3], cur[3], Hs[3], Ws[3], nimg)) return false;
     if (!dump_plane(h, hook, user, "m_body", cur[3], dim << 3, P[3])) return false;
     for (int k = 0; k < 3; ++k) {
         const std::string name = STAGE[4 + k];
@@ -577,20 +580,20 @@ bool walk(scunet_hip* h, const float* x, int hh, int ww, int H, int Wd, float* y
         g.C = cur[lvl]; g.M = P[lvl + 1]; g.N = 4 * co; g.K = ci; g.in_w = Ws[lvl + 1]; g.cout = co;
         if (!run_gemm(h, "up2x2", g, A_ADD2, E_D2S)) return false;
         if (!dump_plane(h, hook, user, ("m_" + name + "_up").c_str(), cur[lvl], co, P[lvl])) return false;
-        if (!stage_blocks(h, "m_" + name + ".", 1, wt.config[4 + k], cur[lvl], Hs[lvl], Ws[lvl])) return false;
+        if (!stage_blocks(h, "m_" + name + ".", 1, wt.config[4 + k], cur[lvl], Hs[lvl], Ws[lvl], nimg)) return false;
         if (!dump_plane(h, hook, user, ("m_" + name).c_str(), cur[lvl], co, P[lvl])) return false;
     }
     h->tag.clear();
     {
         Span sp(h, "head", 2.0 * 9 * in_nc * dim * double(P[0]), 4.0 * (in_nc + 2 * dim) * double(P[0]));
-        if (!head_conv(x, in_nc, hh, ww, H, Wd, W(h, "m_head.0.weight"), dim, cur[0], true, h->stream))
+        if (!head_conv(x, in_nc, hh, ww, H, Wd, W(h, "m_head.0.weight"), dim, cur[0], true, h->stream, nimg))
             return fail(h, "m_head: unsupported shape");
         if (!launched(h, "m_head (tail input)")) return false;
     }
     if (!dump_plane(h, hook, user, "m_tail_in", cur[0], dim, P[0])) return false;
     {
         Span sp(h, "tail", 2.0 * 9 * in_nc * dim * double(P[0]), 4.0 * (in_nc + dim) * double(P[0]));
-        if (!tail_conv(cur[0], dim, H, Wd, W(h, "m_tail.0.weight"), in_nc, y, oh, ow, h->stream))
+        if (!tail_conv(cur[0], dim, H, Wd, W(h, "m_tail.0.weight"), in_nc, y, oh, ow, h->stream, nimg))
             return fail(h, "m_tail: unsupported width");
         if (!launched(h, "m_tail")) return false;
     }
@@ -862,14 +865,21 @@ int scunet_hip_run_batch(scunet_hip* h, const float* x, size_t nimg, size_t c, s
             return fail(h, "expected " + std::to_string(h->wt.in_nc) + " channels, got " + std::to_string(c));
         if (nimg == 0) return true;
         size_t hp = pad64(hh), wp = pad64(ww), n = c * hh * ww;
-        if (!preflight(h, hp, wp, n * nimg, false)) return false;
+        if (!preflight(h, hp * nimg, wp, n * nimg, false)) return false;
         float *dx, *dy;
         if (!to_device(h, "io_x", x, n * nimg, &dx)) return false;
         dy = buf(h, "io_y", n * nimg);
         if (!dy) return false;
-        for (size_t i = 0; i < nimg; ++i)
-            if (!walk(h, dx + i * n, int(hh), int(ww), int(hp), int(wp), dy + i * n, int(hh), int(ww), nullptr, nullptr))
-                return false;
+        if (h->direct3x3 || h->unfused_msa) {
+            // The A/B kernels take one image at a time.
+            for (size_t i = 0; i < nimg; ++i)
+                if (!walk(h, dx + i * n, int(hh), int(ww), int(hp), int(wp), dy + i * n, int(hh), int(ww), nullptr,
+                          nullptr))
+                    return false;
+        } else if (!walk(h, dx, int(hh), int(ww), int(hp), int(wp), dy, int(hh), int(ww), nullptr, nullptr,
+                         int(nimg))) {
+            return false;
+        }
         return to_host(h, y, dy, n * nimg);
     });
 }

@@ -1,7 +1,11 @@
 // Launchers for the gfx950 kernels (kernels.hip). Host code only sees these.
 //
 // Activation layout on the device is pixel-major ("NHWC"): element (pixel p, channel c)
-// of a plane with row stride ld lives at base[p * ld + c], p = y * W + x. A block's
+// of a plane with row stride ld lives at base[p * ld + c], p = y * W + x.
+// Several images are one plane stacked along y: image b owns rows [b img_h, (b + 1) img_h).
+// The spatial kernels (3x3 convolutions, windows, head, tail) take img_h and treat each
+// image's edges as plane edges; per-pixel kernels and the 2x2 convolutions need nothing
+// (img_h is even at every level, so 2x2 pairs never straddle two images). A block's
 // conv half and transformer half are the column ranges [0, t) and [t, 2t) of one
 // [P][2t] buffer, so the split and the concatenation of the reference
 // (cpu.rs:867-868) cost nothing.
@@ -116,6 +120,7 @@ struct Conv3Args {
     float* out = nullptr;
     long ldo = 0;
     int H = 0, W = 0, cin = 0, cout = 0;
+    int img_h = 0;                 // rows per image (0: the whole plane is one image)
     int cblock = 0;                // Winograd: output channels per unit (0 = 32 below 256 input channels, else 16; 16)
     const half_t* w16 = nullptr;   // fp16 mode: [9][cout][cin] k-permuted (conv3x3_h16)
 };
@@ -173,7 +178,8 @@ struct MsaArgs {
     const half_t* h0 = nullptr;
     const half_t* h2 = nullptr;
     int t = 0;
-    int nwh = 0, nww = 0, H = 0, W = 0, shift = 0;
+    int nwh = 0, nww = 0, H = 0, W = 0, shift = 0;   // nwh, H: one image's window rows and rows
+    int nimg = 1;                                     // images stacked along y
     float scale = 0.f;
 };
 // t = 32 (one wave per window, all heads) or 64, 128, 256 (one workgroup per window, one
@@ -187,12 +193,14 @@ void build_attn_table(const float* rp, int heads, float* tab);
 // m_head (in_nc -> dim, 3x3, zero pad) reading an NCHW image of size hh x ww that is
 // replicate-padded on the fly to H x W; writes (or, with add, accumulates into) the
 // pixel-major [H*W][dim] plane.
+// With nimg > 1, x holds nimg such images back to back and out their stacked planes.
 bool head_conv(const float* x, int cin, int hh, int ww, int H, int W, const float* w, int dim,
-               float* out, bool add, hipStream_t s);
+               float* out, bool add, hipStream_t s, int nimg = 1);
 // m_tail (dim -> cout, 3x3, zero pad) from pixel-major [H*W][dim] into NCHW [cout][oh][ow]
 // for the top-left oh x ow corner (oh <= H, ow <= W: the crop is fused).
+// With nimg > 1, in holds nimg stacked H x W planes and out nimg [cout][oh][ow] images.
 bool tail_conv(const float* in, int dim, int H, int W, const float* w, int cout, float* out,
-               int oh, int ow, hipStream_t s);
+               int oh, int ow, hipStream_t s, int nimg = 1);
 
 // A streaming copy of n float4 (the counter-calibration kernel).
 void copy_f4(const void* src, void* dst, long n, hipStream_t s);

@@ -1360,6 +1360,10 @@ __global__ __launch_bounds__(256) void k_conv3x3(Conv3Args a) {
 }
 
 bool conv3x3(const Conv3Args& a, bool relu, hipStream_t s, const char** why) {
+    if (a.img_h > 0 && a.img_h < a.H) {
+        *why = "conv3x3: the direct kernel does not take stacked images";
+        return false;
+    }
     if (a.cin % 16 != 0) { *why = "conv3x3: cin must be a multiple of 16"; return false; }
     long tiles = long((a.W + 15) / 16) * ((a.H + 15) / 16);
     if (a.cout % 64 == 0) {
@@ -1414,7 +1418,7 @@ DEVI WinoUnit wino_unit(long u, int tx, int nb, long tiles, int cbw = 16) {
     return w;
 }
 
-template <bool RELU>
+template <bool RELU, bool BATCH>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_wino(Conv3Args a, long tiles,
                                                                                          long units) {
     // Halo pixel (py, px) at Hs[(py * HP + px) * LDC]: 5 slots per pixel and 24-pixel rows
@@ -1499,12 +1503,24 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             else if (un < units) load(hnxt, nxt.co0, 0);
             // T = B^T d column by column (each needs one column of the patch), then row i
             // of V = T B feeds the products for xi = 4i .. 4i+3 (channels 4lg .. 4lg+3).
+            // Stacked images: the patch row above a tile that starts an image, or below one
+            // that ends it, belongs to the neighbouring image and reads as zero padding.
+            bool mtop = false, mbot = false;
+            if constexpr (BATCH) {
+                const int yo = cur.y0 + 2 * tr;
+                mtop = yo % a.img_h == 0;
+                mbot = (yo + 2) % a.img_h == 0;
+            }
             f4 t[4][4];
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const float* col = &Hs[((2 * tr) * HP + 2 * tc + j) * LDC + lg * 4];
-                const f4 d0 = ld4(col), d1 = ld4(col + HP * LDC), d2 = ld4(col + 2 * HP * LDC),
-                         d3 = ld4(col + 3 * HP * LDC);
+                f4 d0 = ld4(col), d1 = ld4(col + HP * LDC), d2 = ld4(col + 2 * HP * LDC),
+                   d3 = ld4(col + 3 * HP * LDC);
+                if constexpr (BATCH) {
+                    if (mtop) d0 = f4{0.f, 0.f, 0.f, 0.f};
+                    if (mbot) d3 = f4{0.f, 0.f, 0.f, 0.f};
+                }
                 t[0][j] = d0 - d2;
                 t[1][j] = d1 + d2;
                 t[2][j] = d2 - d1;
@@ -1568,7 +1584,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 // outputs of its rows; the pair exchanges the partials of one channel block each through
 // LDS, and each wave finishes (ReLU or residual) and stores one block.
 // ---------------------------------------------------------------------------
-template <bool RELU, bool URES>
+template <bool RELU, bool URES, bool BATCH>
 __global__ __launch_bounds__(512) void k_wino2(Conv3Args a, long tiles, long units) {
     // Two LDS buffers (halo + U each): slice k + 1 is written into one while slice k is read
     // from the other, so a slice costs one barrier. 18-pixel halo rows keep both buffers
@@ -1638,14 +1654,22 @@ __global__ __launch_bounds__(512) void k_wino2(Conv3Args a, long tiles, long uni
     // acc[cb][ii][j]: M[2hh + ii][j] for channel block cb (co0 + 16 cb + 4lg .. +3).
     f4 acc[2][2][4];
     // One slice: the two rows of V = B^T d B this half owns, then 2 x 4 x 2 x 4 products.
-    auto slice = [&](auto HHc, const float* buf, int ci0) {
+    auto slice = [&](auto HHc, const float* buf, int ci0, bool mrow) {
         constexpr int H2 = decltype(HHc)::value;
         const float* Us = buf + HSZ;
         f4 t[2][4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const float* col = &buf[((2 * tr + H2) * HP + 2 * tc + j) * LDC + lg * 4];
-            const f4 da = ld4(col), db = ld4(col + HP * LDC), dc = ld4(col + 2 * HP * LDC);
+            f4 da = ld4(col), db = ld4(col + HP * LDC), dc = ld4(col + 2 * HP * LDC);
+            // Stacked images: patch row 0 (H2 = 0: da) above a tile that starts an image, or
+            // row 3 (H2 = 1: dc) below one that ends it, reads as zero padding.
+            if constexpr (BATCH) {
+                if (mrow) {
+                    if constexpr (H2 == 0) da = f4{0.f, 0.f, 0.f, 0.f};
+                    else dc = f4{0.f, 0.f, 0.f, 0.f};
+                }
+            }
             if constexpr (H2 == 0) {         // rows d0, d1, d2: T0 = d0 - d2, T1 = d1 + d2
                 t[0][j] = da - dc;
                 t[1][j] = db + dc;
@@ -1778,8 +1802,13 @@ __global__ __launch_bounds__(512) void k_wino2(Conv3Args a, long tiles, long uni
                 if (c + 1 == nch) load_res(cur, res);
             }
             const float* buf = lds + kb * BSZ;
-            if (hh == 0) slice(std::integral_constant<int, 0>{}, buf, c * BK);
-            else slice(std::integral_constant<int, 1>{}, buf, c * BK);
+            bool mrow = false;
+            if constexpr (BATCH) {
+                const int yo = cur.y0 + 2 * tr;
+                mrow = hh == 0 ? yo % a.img_h == 0 : (yo + 2) % a.img_h == 0;
+            }
+            if (hh == 0) slice(std::integral_constant<int, 0>{}, buf, c * BK, mrow);
+            else slice(std::integral_constant<int, 1>{}, buf, c * BK, mrow);
             if (more) stash(lds + (kb ^ 1) * BSZ);
             __syncthreads();
             kb ^= 1;
@@ -1801,19 +1830,8 @@ __global__ __launch_bounds__(512) void k_wino2(Conv3Args a, long tiles, long uni
     }
 }
 
-bool conv3x3_winograd(const Conv3Args& a, bool relu, hipStream_t s, const char** why) {
-    if (a.cin % 16 != 0 || a.cout % 16 != 0 || (a.H & 1) || (a.W & 1)) {
-        *why = "conv3x3_winograd: cin and cout must be multiples of 16 and the plane even";
-        return false;
-    }
-    if (double(a.H) * a.W * a.ldi >= 4294967296.0 || double(a.cout) * a.cin * 16 >= 4294967296.0) {
-        *why = "conv3x3_winograd: plane too large for 32-bit element offsets";
-        return false;
-    }
-    // 32 output channels per unit, except at cin >= 256 (level 3 of the forward), where the
-    // 16-channel kernel measured faster (238 against 247 us per launch at 1080p).
-    const bool wide = a.cout % 32 == 0 && a.cin >= 32 && a.cin < 256 && a.cblock != 16;
-    const bool ures = wide && a.cin == 32 && a.cout == 32;
+template <bool BATCH>
+static bool launch_wino(const Conv3Args& a, bool relu, bool wide, bool ures, hipStream_t s, const char** why) {
     static int per_cu[6] = {-1, -1, -1, -1, -1, -1}, cus = 0;
     int& pc = per_cu[(relu ? 1 : 0) + (ures ? 4 : wide ? 2 : 0)];
     if (pc < 0) {
@@ -1822,13 +1840,14 @@ bool conv3x3_winograd(const Conv3Args& a, bool relu, hipStream_t s, const char**
         if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
         if (e == hipSuccess) {
             if (ures)
-                e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&pc, relu ? k_wino2<true, true> : k_wino2<false, true>,
-                                                                 512, 0);
+                e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                    &pc, relu ? k_wino2<true, true, BATCH> : k_wino2<false, true, BATCH>, 512, 0);
             else if (wide)
-                e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&pc, relu ? k_wino2<true, false> : k_wino2<false, false>,
-                                                                 512, 0);
+                e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                    &pc, relu ? k_wino2<true, false, BATCH> : k_wino2<false, false, BATCH>, 512, 0);
             else
-                e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&pc, relu ? k_wino<true> : k_wino<false>, 256, 0);
+                e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                    &pc, relu ? k_wino<true, BATCH> : k_wino<false, BATCH>, 256, 0);
         }
         if (e != hipSuccess) {
             *why = "conv3x3_winograd: device query failed";
@@ -1845,18 +1864,39 @@ bool conv3x3_winograd(const Conv3Args& a, bool relu, hipStream_t s, const char**
     dim3 g{unsigned(grid), 1u, 1u};
     if (ures) {
         dim3 block{512u, 1u, 1u};
-        if (relu) hipLaunchKernelGGL((k_wino2<true, true>), g, block, 0, s, a, tiles, units);
-        else hipLaunchKernelGGL((k_wino2<false, true>), g, block, 0, s, a, tiles, units);
+        if (relu) hipLaunchKernelGGL((k_wino2<true, true, BATCH>), g, block, 0, s, a, tiles, units);
+        else hipLaunchKernelGGL((k_wino2<false, true, BATCH>), g, block, 0, s, a, tiles, units);
     } else if (wide) {
         dim3 block{512u, 1u, 1u};
-        if (relu) hipLaunchKernelGGL((k_wino2<true, false>), g, block, 0, s, a, tiles, units);
-        else hipLaunchKernelGGL((k_wino2<false, false>), g, block, 0, s, a, tiles, units);
+        if (relu) hipLaunchKernelGGL((k_wino2<true, false, BATCH>), g, block, 0, s, a, tiles, units);
+        else hipLaunchKernelGGL((k_wino2<false, false, BATCH>), g, block, 0, s, a, tiles, units);
     } else {
         dim3 block{256u, 1u, 1u};
-        if (relu) hipLaunchKernelGGL(k_wino<true>, g, block, 0, s, a, tiles, units);
-        else hipLaunchKernelGGL(k_wino<false>, g, block, 0, s, a, tiles, units);
+        if (relu) hipLaunchKernelGGL((k_wino<true, BATCH>), g, block, 0, s, a, tiles, units);
+        else hipLaunchKernelGGL((k_wino<false, BATCH>), g, block, 0, s, a, tiles, units);
     }
     return true;
+}
+
+bool conv3x3_winograd(const Conv3Args& a, bool relu, hipStream_t s, const char** why) {
+    if (a.cin % 16 != 0 || a.cout % 16 != 0 || (a.H & 1) || (a.W & 1)) {
+        *why = "conv3x3_winograd: cin and cout must be multiples of 16 and the plane even";
+        return false;
+    }
+    if (double(a.H) * a.W * a.ldi >= 4294967296.0 || double(a.cout) * a.cin * 16 >= 4294967296.0) {
+        *why = "conv3x3_winograd: plane too large for 32-bit element offsets";
+        return false;
+    }
+    const bool batch = a.img_h > 0 && a.img_h < a.H;
+    if (batch && ((a.img_h & 1) || a.H % a.img_h != 0)) {
+        *why = "conv3x3_winograd: stacked images must have an even height that divides the plane";
+        return false;
+    }
+    // 32 output channels per unit, except at cin >= 256 (level 3 of the forward), where the
+    // 16-channel kernel measured faster (238 against 247 us per launch at 1080p).
+    const bool wide = a.cout % 32 == 0 && a.cin >= 32 && a.cin < 256 && a.cblock != 16;
+    const bool ures = wide && a.cin == 32 && a.cout == 32;
+    return batch ? launch_wino<true>(a, relu, wide, ures, s, why) : launch_wino<false>(a, relu, wide, ures, s, why);
 }
 
 // ---------------------------------------------------------------------------
@@ -1897,6 +1937,9 @@ __global__ __launch_bounds__(NWV * 64) void k_conv3h(Conv3Args a, int tiles_x, l
     if (ti >= tiles) return;   // no barrier is reached by any wave of this workgroup
     const int ty = int(ti / tiles_x), tx = int(ti - long(ty) * tiles_x);
     const int y0 = ty * R, x0 = tx * TW;
+    // The rows of this tile's image (R divides the image height: a tile never straddles).
+    const int ih = a.img_h > 0 ? a.img_h : a.H;
+    const int ylo = (y0 / ih) * ih, yhi = ylo + ih;
 
     // Filter fragments: A[tap][j] = W[tap][cog*32 + 16j + li][32kk + 8lg .. (k-permuted)].
     h8 wa[NA][9][2];
@@ -1917,7 +1960,7 @@ __global__ __launch_bounds__(NWV * 64) void k_conv3h(Conv3Args a, int tiles_x, l
         const int hr = p / RP, hc = p - hr * RP;
         const int gy = y0 - 1 + hr, gx = x0 - 1 + hc;
         h8 v = h8{0, 0, 0, 0, 0, 0, 0, 0};
-        if (gy >= 0 && gy < a.H && gx >= 0 && gx < a.W) {
+        if (gy >= ylo && gy < yhi && gx >= 0 && gx < a.W) {
             const float* src = a.in + (long(gy) * a.W + gx) * a.ldi + 32 * (q >> 2) + 4 * (q & 3);
             v = pack8(ld4(src), ld4(src + 16));
         }
@@ -1990,6 +2033,10 @@ static void launch_conv3h(const Conv3Args& a, bool relu, hipStream_t s) {
 bool conv3x3_h16(const Conv3Args& a, bool relu, hipStream_t s, const char** why) {
     if (!a.w16 || a.cin != a.cout) {
         *why = "conv3x3_h16: needs the k-permuted fp16 filters and cin == cout";
+        return false;
+    }
+    if (a.img_h > 0 && (a.img_h % 8 != 0 || a.H % a.img_h != 0)) {
+        *why = "conv3x3_h16: stacked images must be a multiple of 8 rows high";
         return false;
     }
     if (a.H <= 0 || a.W <= 0) return true;
@@ -2231,14 +2278,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(T == 32 ? 2
     const int li = lane & 15, lg = lane >> 4;
     const long wi = long(blockIdx.x) * 4 + wave;
     const bool valid = wi < nw;
-    const int wh = valid ? int(wi / a.nww) : 0, ww = valid ? int(wi - long(wh) * a.nww) : 0;
+    // Window wi = (image, window row, window column); the roll wraps within the image.
+    const int wpi = a.nwh * a.nww;
+    const int img = valid ? int(wi / wpi) : 0;
+    const int wr = valid ? int(wi - long(img) * wpi) : 0;
+    const int wh = wr / a.nww, ww = wr - wh * a.nww;
+    const long ybase = long(img) * a.H;
     ET* xw = xs + wave * 64 * LDX;
     auto rowof = [&](int t) -> long {
         int y = wh * 8 + (t >> 3) + a.shift;
         int x = ww * 8 + (t & 7) + a.shift;
         if (y >= a.H) y -= a.H;
         if (x >= a.W) x -= a.W;
-        return long(y) * a.W + x;
+        return (ybase + y) * a.W + x;
     };
 
     // 1. LN1 of the window's tokens into LDS.
@@ -2612,13 +2664,18 @@ __global__ __launch_bounds__(T * 2) __attribute__((amdgpu_waves_per_eu(2, 2))) v
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int li = lane & 15, lg = lane >> 4;
     const long wi = blockIdx.x;
-    const int wh = int(wi / a.nww), ww = int(wi - long(wh) * a.nww);
+    // Window wi = (image, window row, window column); the roll wraps within the image.
+    const int wpi = a.nwh * a.nww;
+    const int img = int(wi / wpi);
+    const int wr = int(wi - long(img) * wpi);
+    const int wh = wr / a.nww, ww = wr - wh * a.nww;
+    const long ybase = long(img) * a.H;
     auto rowof = [&](int t) -> long {
         int y = wh * 8 + (t >> 3) + a.shift;
         int x = ww * 8 + (t & 7) + a.shift;
         if (y >= a.H) y -= a.H;
         if (x >= a.W) x -= a.W;
-        return long(y) * a.W + x;
+        return (ybase + y) * a.W + x;
     };
 
     // 1. LN1 (cpu.rs:338-357) of token tiles 16m .. 16m + 15, m = wave, wave + HEADS, ...
@@ -3008,7 +3065,7 @@ static bool launch_msa(const MsaArgs& a, long nw, hipStream_t s, const char** wh
 }
 
 bool msa_fused(const MsaArgs& a, hipStream_t s, const char** why) {
-    const long nw = long(a.nwh) * a.nww;
+    const long nw = long(a.nwh) * a.nww * a.nimg;
     if (nw == 0) return true;
     if (a.w0 && a.t != 32 && a.t != 64) {
         *why = "msa_fused: the fused MLP is available at t = 32, 64";
@@ -3057,6 +3114,7 @@ void build_attn_table(const float* rp, int heads, float* tab) {
 __global__ __launch_bounds__(256) void k_head(const float* __restrict__ x, int cin, int hh, int ww, int H,
                                               int W, const float* __restrict__ w, float* __restrict__ out,
                                               int add, long P) {
+    // P = nimg H W: image b is rows [b H, (b + 1) H) of the output plane and x + b cin hh ww.
     constexpr int LDW = 36;
     __shared__ float sw[64 * LDW];            // W[co][k], k = ci*9 + tap, zero beyond cin*9
     const int K = cin * 9;
@@ -3074,7 +3132,9 @@ __global__ __launch_bounds__(256) void k_head(const float* __restrict__ x, int c
         for (int kg = 0; kg < 2; ++kg) wf[nt][kg] = ld4(&sw[(nt * 16 + li) * LDW + kg * 16 + lg * 4]);
     for (int step = 0; step < 4; ++step) {
         const long p = (long(blockIdx.x) * 16 + wave * 4 + step) * 16 + li;
-        const int y = int(p / W), xx = int(p - long(y) * W);
+        const int yy = int(p / W), xx = int(p - long(yy) * W);
+        const int b = yy / H, y = yy - b * H;
+        const float* xb = x + long(b) * cin * hh * ww;
         f4 av[2];
 #pragma unroll
         for (int kg = 0; kg < 2; ++kg)
@@ -3086,7 +3146,7 @@ __global__ __launch_bounds__(256) void k_head(const float* __restrict__ x, int c
                     const int ci = k / 9, tap = k - ci * 9;
                     const int sy = y + tap / 3 - 1, sx = xx + tap % 3 - 1;
                     if (sy >= 0 && sy < H && sx >= 0 && sx < W)
-                        v = x[(long(ci) * hh + (sy < hh ? sy : hh - 1)) * ww + (sx < ww ? sx : ww - 1)];
+                        v = xb[(long(ci) * hh + (sy < hh ? sy : hh - 1)) * ww + (sx < ww ? sx : ww - 1)];
                 }
                 av[kg][s] = v;
             }
@@ -3108,9 +3168,9 @@ __global__ __launch_bounds__(256) void k_head(const float* __restrict__ x, int c
 }
 
 bool head_conv(const float* x, int cin, int hh, int ww, int H, int W, const float* w, int dim,
-               float* out, bool add, hipStream_t s) {
-    if (dim != 64 || cin * 9 > 32) return false;
-    const long P = long(H) * W;
+               float* out, bool add, hipStream_t s, int nimg) {
+    if (dim != 64 || cin * 9 > 32 || nimg < 1) return false;
+    const long P = long(H) * W * nimg;
     hipLaunchKernelGGL(k_head, dim3(unsigned((P + 255) / 256)), dim3(256), 0, s, x, cin, hh, ww, H, W, w, out,
                        add ? 1 : 0, P);
     return true;
@@ -3129,8 +3189,12 @@ __global__ __launch_bounds__(256) void k_tail(const float* __restrict__ in, int 
                                               int ow) {
     constexpr int HW = 18, CH = 16, LDC = CH + 4, DIM = 64;
     __shared__ float hs[HW * HW * LDC];
+    // Stacked images: tile rows y0 .. y0 + 15 of the plane lie in image b (16 divides H).
     const int tx = (W + 15) / 16;
-    const int y0 = int(blockIdx.x / tx) * 16, x0 = int(blockIdx.x % tx) * 16;
+    const int ys = int(blockIdx.x / tx) * 16, x0 = int(blockIdx.x % tx) * 16;
+    const int b = ys / H, y0 = ys - b * H;
+    in += long(b) * H * W * DIM;
+    out += long(b) * COUT * oh * ow;
     const int ly = threadIdx.x >> 4, lx = threadIdx.x & 15;
     float acc[COUT];
 #pragma unroll
@@ -3167,9 +3231,9 @@ __global__ __launch_bounds__(256) void k_tail(const float* __restrict__ in, int 
 }
 
 bool tail_conv(const float* in, int dim, int H, int W, const float* w, int cout, float* out, int oh,
-               int ow, hipStream_t s) {
-    if (dim != 64) return false;
-    const unsigned tiles = unsigned(((W + 15) / 16) * ((H + 15) / 16));
+               int ow, hipStream_t s, int nimg) {
+    if (dim != 64 || nimg < 1 || (nimg > 1 && H % 16 != 0)) return false;
+    const unsigned tiles = unsigned(((W + 15) / 16) * ((H + 15) / 16) * nimg);
     if (cout == 3) hipLaunchKernelGGL(k_tail<3>, dim3(tiles), dim3(256), 0, s, in, H, W, w, out, oh, ow);
     else if (cout == 1) hipLaunchKernelGGL(k_tail<1>, dim3(tiles), dim3(256), 0, s, in, H, W, w, out, oh, ow);
     else return false;

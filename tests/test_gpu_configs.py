@@ -321,12 +321,27 @@ def test_device_need_is_exact_and_refuses_before_allocating(weights_path):
         assert be.footprint() == before
 
 
-def test_run_batch_equals_single_runs(weights_path):
+@pytest.mark.parametrize("n,h,w", [(3, 72, 80), (5, 64, 64), (3, 64, 72), (2, 200, 136), (1, 64, 64)])
+def test_run_batch_equals_single_runs(weights_path, n, h, w):
+    """Several images per launch, stacked along y: every image's result is bit-identical to
+    its own forward. 64-row images put an image edge inside the 16-row Winograd units at the
+    1/8 level (8 rows per image there), 72x80 / 200x136 pad to 128 / 256 rows (units aligned
+    to the images), 64x72 pads the width to 128."""
     from scunet_hip import Hip, synth
-    xs = np.stack([synth.noisy_image(10 + i, 3, 72, 80, 25) for i in range(3)])
+    xs = np.stack([synth.noisy_image(10 + i, 3, h, w, 25) for i in range(n)])
     with Hip(weights_path) as be:
         ys = be.run_batch(xs)
-        for i in range(3):
+        for i in range(n):
+            assert np.array_equal(ys[i], be.run_fused(xs[i])), i
+
+
+def test_run_batch_fp16_equals_single_runs(weights_path):
+    from scunet_hip import Hip, synth
+    xs = np.stack([synth.noisy_image(20 + i, 3, 64, 64, 25) for i in range(4)])
+    with Hip(weights_path) as be:
+        be.set_precision("fp16")
+        ys = be.run_batch(xs)
+        for i in range(4):
             assert np.array_equal(ys[i], be.run_fused(xs[i])), i
 
 
