@@ -2040,11 +2040,13 @@ bool conv3x3_h16(const Conv3Args& a, bool relu, hipStream_t s, const char** why)
         return false;
     }
     if (a.H <= 0 || a.W <= 0) return true;
+    // 256 channels: 8-row tiles, so each streamed filter block feeds twice the pixels (level 3
+    // of the 1080p forward: 87 -> 59 us per launch).
     switch (a.cin) {
         case 32: launch_conv3h<32, 8, 4>(a, relu, s); break;
         case 64: launch_conv3h<64, 8, 4>(a, relu, s); break;
         case 128: launch_conv3h<128, 8, 4>(a, relu, s); break;
-        case 256: launch_conv3h<256, 4, 8>(a, relu, s); break;
+        case 256: launch_conv3h<256, 8, 8>(a, relu, s); break;
         default: *why = "conv3x3_h16: channels must be 32, 64, 128 or 256"; return false;
     }
     return true;
