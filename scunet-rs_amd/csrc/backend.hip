@@ -149,8 +149,10 @@ struct Span {
     }
     hipEvent_t next() {
         if (h->ev_used == h->ev_pool.size()) {
+            // Timing-only events: no system-scope fence (cache writeback and invalidate) at
+            // each record; the report synchronizes the stream before reading them.
             hipEvent_t e;
-            hipEventCreate(&e);
+            hipEventCreateWithFlags(&e, hipEventDisableSystemFence);
             h->ev_pool.push_back(e);
         }
         return h->ev_pool[h->ev_used++];
