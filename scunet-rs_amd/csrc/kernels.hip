@@ -11,6 +11,7 @@
 // as A and B agree on it.
 #include "kernels.h"
 
+#include <atomic>
 #include <type_traits>
 
 #include <algorithm>
@@ -627,19 +628,36 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     }
 }
 
-template <int MT, int BN, int KC, int AM, int EP, bool H16>
-static void launch_gemm3_k(const GemmArgs& g, hipStream_t s) {
-    static int per_cu = -1, cus = 0;
-    if (per_cu < 0) {
+// Persistent grids size themselves to the chip: CU count and resident workgroups per CU of
+// a kernel, queried at its first launch and kept in relaxed atomics (handles on several
+// threads may launch concurrently; they compute and store the same values).
+struct Occ {
+    int cus, per_cu;
+};
+template <typename K>
+static bool query_occ(K kernel, int threads, std::atomic<int>& cus_c, std::atomic<int>& pc_c, Occ* o) {
+    int cus = cus_c.load(std::memory_order_relaxed), pc = pc_c.load(std::memory_order_relaxed);
+    if (cus < 1 || pc < 1) {
         int dev = 0;
         if (hipGetDevice(&dev) != hipSuccess ||
             hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_gemm3<MT, BN, KC, AM, EP, H16>, 256, 0) !=
-                hipSuccess)
-            per_cu = 1;
-        if (per_cu < 1) per_cu = 1;
-        if (cus < 1) cus = 256;
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&pc, kernel, threads, 0) != hipSuccess)
+            return false;
+        cus = std::max(cus, 1);
+        pc = std::max(pc, 1);
+        cus_c.store(cus, std::memory_order_relaxed);
+        pc_c.store(pc, std::memory_order_relaxed);
     }
+    *o = Occ{cus, pc};
+    return true;
+}
+
+template <int MT, int BN, int KC, int AM, int EP, bool H16>
+static void launch_gemm3_k(const GemmArgs& g, hipStream_t s) {
+    static std::atomic<int> cus_c{0}, pc_c{0};
+    Occ oc;
+    if (!query_occ(k_gemm3<MT, BN, KC, AM, EP, H16>, 256, cus_c, pc_c, &oc)) oc = Occ{256, 1};
+    const int cus = oc.cus, per_cu = oc.per_cu;
     const long mtiles = (g.M + 64 * MT - 1) / (64 * MT);
     const long tiles = ((mtiles + 7) / 8) * 8 * (g.N / BN);
     dim3 grid{unsigned(std::min<long>(tiles, long(cus) * per_cu)), 1u, 1u}, block{256u, 1u, 1u};
@@ -961,16 +979,10 @@ __global__ __launch_bounds__(NW * 64) void k_pconv(PconvArgs a) {
 
 template <int C, int MT, int NW, int MODE, bool RPRE, bool H16 = false>
 static bool launch_pconv(const PconvArgs& a, hipStream_t s) {
-    static int per_cu = -1, cus = 0;
-    if (per_cu < 0) {
-        int dev = 0;
-        if (hipGetDevice(&dev) != hipSuccess) return false;
-        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return false;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_pconv<C, MT, NW, MODE, RPRE, H16>, NW * 64, 0) !=
-            hipSuccess)
-            return false;
-        if (per_cu < 1) per_cu = 1;
-    }
+    static std::atomic<int> cus_c{0}, pc_c{0};
+    Occ oc;
+    if (!query_occ(k_pconv<C, MT, NW, MODE, RPRE, H16>, NW * 64, cus_c, pc_c, &oc)) return false;
+    const int cus = oc.cus, per_cu = oc.per_cu;
     const long groups = (a.M + 16 * MT - 1) / (16 * MT);
     const long waves = std::min<long>(groups, long(cus) * per_cu * NW);
     dim3 grid{unsigned((waves + NW - 1) / NW), 1u, 1u}, block{unsigned(NW * 64), 1u, 1u};
@@ -1832,29 +1844,18 @@ __global__ __launch_bounds__(512) void k_wino2(Conv3Args a, long tiles, long uni
 
 template <bool BATCH>
 static bool launch_wino(const Conv3Args& a, bool relu, bool wide, bool ures, hipStream_t s, const char** why) {
-    static int per_cu[6] = {-1, -1, -1, -1, -1, -1}, cus = 0;
-    int& pc = per_cu[(relu ? 1 : 0) + (ures ? 4 : wide ? 2 : 0)];
-    if (pc < 0) {
-        int dev = 0;
-        hipError_t e = hipGetDevice(&dev);
-        if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-        if (e == hipSuccess) {
-            if (ures)
-                e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
-                    &pc, relu ? k_wino2<true, true, BATCH> : k_wino2<false, true, BATCH>, 512, 0);
-            else if (wide)
-                e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
-                    &pc, relu ? k_wino2<true, false, BATCH> : k_wino2<false, false, BATCH>, 512, 0);
-            else
-                e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
-                    &pc, relu ? k_wino<true, BATCH> : k_wino<false, BATCH>, 256, 0);
-        }
-        if (e != hipSuccess) {
-            *why = "conv3x3_winograd: device query failed";
-            return false;
-        }
-        if (pc < 1) pc = 1;
+    static std::atomic<int> cus_c[6] = {}, pc_c[6] = {};
+    const int v = (relu ? 1 : 0) + (ures ? 4 : wide ? 2 : 0);
+    void (*kern)(Conv3Args, long, long) =
+        ures ? (relu ? k_wino2<true, true, BATCH> : k_wino2<false, true, BATCH>)
+             : wide ? (relu ? k_wino2<true, false, BATCH> : k_wino2<false, false, BATCH>)
+                    : (relu ? k_wino<true, BATCH> : k_wino<false, BATCH>);
+    Occ oc;
+    if (!query_occ(kern, ures || wide ? 512 : 256, cus_c[v], pc_c[v], &oc)) {
+        *why = "conv3x3_winograd: device query failed";
+        return false;
     }
+    const int cus = oc.cus, pc = oc.per_cu;
     const long tiles = long((a.W + 15) / 16) * ((a.H + 15) / 16);
     const int nb = a.cout / (wide ? 32 : 16);
     // Units are numbered 8 j + xcd with j < ceil(tiles / 8) * nb; numbers whose tile is

@@ -374,3 +374,30 @@ def test_config4_gray_4096_full_size(weights_path_gray):
             want = O.conv_trans_block(owt, "m_down1.1", band, shift)[:, m:-m]
             assert max_abs(want, got[:, r0:r1]) <= STAGE_TOL, shift
             assert np.isfinite(got).all()
+
+
+def test_two_handles_on_two_threads(weights_path):
+    """The threading contract of the boundary (one handle per thread, each with its own
+    stream; cuda.rs's `Cuda` is likewise single-threaded): two handles forwarding
+    concurrently from two threads (ctypes releases the GIL during the calls) give the same
+    bits as one after the other."""
+    import threading
+    from scunet_hip import Hip, synth
+    xs = [synth.noisy_image(30 + i, 3, 96, 128, 25) for i in range(2)]
+    hs = [Hip(weights_path) for _ in range(2)]
+    got = [None, None]
+    try:
+        def work(i):
+            got[i] = [hs[i].run_fused(xs[i]) for _ in range(3)]
+        ts = [threading.Thread(target=work, args=(i,)) for i in range(2)]
+        for t in ts:
+            t.start()
+        for t in ts:
+            t.join()
+        for i in range(2):
+            want = hs[i].run_fused(xs[i])
+            for y in got[i]:
+                assert np.array_equal(y, want), i
+    finally:
+        for h in hs:
+            h.close()
