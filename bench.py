@@ -10,9 +10,10 @@ contract with pad and crop fused into the first and last convolution).
 
 value = 1920*1080 input pixels / mean step time, in Mpx/s (the reference counts input
 pixels, examples/bench.rs:191). Per-kernel device times come from HIP event pairs that
-the library records around every launch on its own stream during the timed steps.
+the library records around every launch on its own stream during the timed steps; the
+fp16-operand mode is timed after them and reported in its own sub-object (fp16_mode).
 
-Usage: python bench.py [--gpus 1] [--steps 10] [--warmup 3] [--no-cpu-baseline]
+Usage: python bench.py [--gpus 1] [--steps 10] [--warmup 5] [--no-cpu-baseline] [--no-fp16]
 """
 import argparse
 import json
@@ -123,7 +124,7 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-rows", type=int, default=512,
                     help="rows of the 1080p input the CPU baseline forwards (a multiple of 8)")
