@@ -52,6 +52,9 @@ const char* scunet_hip_name(const scunet_hip* h);
 /* The architecture read from the checkpoint (weights.rs:84-98). config has 7 entries. */
 int scunet_hip_arch(const scunet_hip* h, int* in_nc, int* dim, int* head_dim, int* window,
                     int* config);
+/* The checkpoint's variant, one of the eight published names (Weights::arch.name(),
+ * weights.rs:62-73), e.g. "color-real-psnr"; "" for a null handle. */
+const char* scunet_hip_variant(const scunet_hip* h);
 
 /* --- arithmetic mode (no counterpart in the reference, whose GPU path is fp32 only) ---
  * SCUNET_HIP_FP32 (the default): every product in fp32, the reference's arithmetic.

@@ -806,6 +806,8 @@ int scunet_hip_arch(const scunet_hip* h, int* in_nc, int* dim, int* head_dim, in
     return 0;
 }
 
+const char* scunet_hip_variant(const scunet_hip* h) { return h ? h->wt.variant.c_str() : ""; }
+
 int scunet_hip_forward_device(scunet_hip* h, const float* x, size_t c, size_t hp, size_t wp, float* y) {
     return guard(h, [&] {
         if (!shape_ok(h, c, hp, wp)) return false;

@@ -23,7 +23,7 @@ LIB_PATH = os.path.join(_HERE, "..", "lib", "libscunet_hip.so")
 # The symbols include/scunet_hip.h declares.
 EXPORTS = [
     "scunet_hip_create", "scunet_hip_create_error", "scunet_hip_destroy", "scunet_hip_last_error",
-    "scunet_hip_name", "scunet_hip_arch", "scunet_hip_set_precision", "scunet_hip_precision",
+    "scunet_hip_name", "scunet_hip_arch", "scunet_hip_variant", "scunet_hip_set_precision", "scunet_hip_precision",
     "scunet_hip_forward", "scunet_hip_forward_device",
     "scunet_hip_forward_dump", "scunet_hip_run", "scunet_hip_run_device", "scunet_hip_run_batch",
     "scunet_hip_device_need", "scunet_hip_footprint",
@@ -66,6 +66,8 @@ def load_library(path=None):
     L.scunet_hip_name.restype = ctypes.c_char_p
     ip = ctypes.POINTER(ctypes.c_int)
     L.scunet_hip_arch.argtypes = [_vp, ip, ip, ip, ip, ip]
+    L.scunet_hip_variant.argtypes = [_vp]
+    L.scunet_hip_variant.restype = ctypes.c_char_p
     L.scunet_hip_set_precision.argtypes = [_vp, ctypes.c_int]
     L.scunet_hip_precision.argtypes = [_vp]
     L.scunet_hip_forward.argtypes = [_vp, _f, _sz, _sz, _sz, _f]
@@ -177,6 +179,7 @@ class Hip:
         self._lib.scunet_hip_arch(h, *[ctypes.byref(v) for v in a], cfg)
         self.in_nc, self.dim, self.head_dim, self.window = (v.value for v in a)
         self.config = list(cfg)
+        self.variant = self._lib.scunet_hip_variant(h).decode()
 
     # -- lifetime --
     def close(self):

@@ -19,6 +19,13 @@ def declared_symbols():
     return sorted(set(re.findall(r"\b(scunet_hip_\w+)\s*\(", text)))
 
 
+def all_declared_symbols():
+    """Every entry point of every header under include/ (the backend and the PNG codec)."""
+    inc = os.path.join(REPO, "include")
+    text = "".join(open(os.path.join(inc, f)).read() for f in sorted(os.listdir(inc)) if f.endswith(".h"))
+    return sorted(set(re.findall(r"\b(scunet_\w+)\s*\(", text)))
+
+
 def test_header_and_python_binding_agree():
     from scunet_hip import EXPORTS
     assert sorted(EXPORTS) == declared_symbols()
@@ -29,11 +36,12 @@ def test_library_exports_every_declared_symbol():
     if not os.path.exists(LIB_PATH):
         pytest.skip("library not built")
     out = subprocess.run(["nm", "-D", "--defined-only", LIB_PATH], capture_output=True, text=True).stdout
-    exported = set(re.findall(r"\bT (scunet_hip_\w+)", out))
-    missing = [s for s in declared_symbols() if s not in exported]
+    exported = set(re.findall(r"\bT (scunet_\w+)", out))
+    assert set(declared_symbols()) < set(all_declared_symbols())
+    missing = [s for s in all_declared_symbols() if s not in exported]
     assert not missing, missing
     lib = ctypes.CDLL(LIB_PATH)          # loads without a GPU: no device call at load time
-    for s in declared_symbols():
+    for s in all_declared_symbols():
         assert hasattr(lib, s)
 
 
