@@ -1,7 +1,8 @@
 """BASELINE's workload configurations on the GPU: the grayscale variant, config 2 at its
 full size against the oracle, the isolated attention operator of config 5 at its real
-window counts, the fused and three-launch attention halves against each other, and
-size-independent properties at the 1080p headline size (config 3)."""
+window counts, the fused and three-launch attention halves against each other, and the
+1080p headline size (config 3): every stage against the oracle, and size-independent
+properties."""
 import os
 
 import numpy as np
@@ -140,6 +141,30 @@ def test_1080p_properties(be):
     y = be.forward(np.ascontiguousarray(pad_replicate(x, plan.hp, plan.wp), dtype=np.float32), plan)
     assert np.array_equal(a, y[:, :h, :w])
     assert 0.0 < float(np.abs(a).mean()) < 10.0
+
+
+def test_config3_1080p_every_stage_against_cpu(be, owt):
+    """The headline workload at its full size against the reference arithmetic: all 16
+    stage planes of the 1088x1920 padded forward (cpu.rs:1175-1321's hook points) and the
+    output within 1e-4. The oracle's forward takes about 40 s on 16 host threads; the planes
+    of both sides are held in host memory (about 4 GB each)."""
+    from scunet_hip import Plan, pad_replicate, synth
+    x = synth.config_input(3)
+    c, h, w = x.shape
+    plan = Plan(h, w)
+    xp = np.ascontiguousarray(pad_replicate(x, plan.hp, plan.wp), dtype=np.float32)
+    got = {}
+    y = be.forward_dump(xp, lambda n, v: got.__setitem__(n, v))
+    want_y, want = O.forward_dump(owt, xp)
+    assert list(got) == list(want) and len(want) == 16
+    worst = {}
+    for name in want:
+        worst[name] = max_abs(want[name], got[name])
+        del got[name]
+    print("config 3 worst |gpu - cpu| per stage:", {k: f"{v:.2e}" for k, v in worst.items()})
+    assert all(d <= STAGE_TOL for d in worst.values()), worst
+    assert max_abs(want_y[:, :h, :w], y[:, :h, :w]) <= STAGE_TOL
+    assert np.array_equal(y[:, :h, :w], be.run_fused(x))
 
 
 def _hip_with(weights_path, env):
