@@ -101,12 +101,15 @@ def _attn_windows_f64(qkv, rp, nwh, nww, c, heads, shift, wins):
     return out
 
 
+@pytest.mark.parametrize("hard", [False, True])
 @pytest.mark.parametrize("level", [0, 1, 2, 3])
-def test_attention_operator_sweep_config5(be, owt, level):
+def test_attention_operator_sweep_config5(be, owt, level, hard):
     """x ~ N(0,1) [nw][64][C] at the 1920x1088 window grid of each level,
     qkv from the level's seeded embedding weights, rel-pos tables ~ N(0, 0.02) laid out as
     upstream's [225][heads] then re-viewed; W and SW. Checked against a float64 evaluation on
-    every window of the last window row and column (where the mask acts) plus a random set."""
+    every window of the last window row and column (where the mask acts) plus a random set.
+    The hard case takes qkv = [x, x, x]: each query meets itself with a logit of |x|^2 / sqrt(32)
+    (about 5.7), so the softmax is sharp rather than nearly uniform."""
     c = 32 << level
     heads = c // 32
     nwh, nww = 136 >> level, 240 >> level
@@ -115,6 +118,8 @@ def test_attention_operator_sweep_config5(be, owt, level):
     x = rng.standard_normal((nw * 64, c), dtype=np.float32)
     name = ["m_down1.0", "m_down2.0", "m_down3.0", "m_body.0"][level] + ".trans_block.msa.embedding_layer"
     qkv = (x @ owt.t[name + ".weight"].T + owt.t[name + ".bias"]).astype(np.float32)
+    if hard:
+        qkv = np.ascontiguousarray(np.concatenate([x, x, x], axis=1))
     raw = np.clip(rng.standard_normal((225, heads)) * 0.02, -0.04, 0.04)
     rp = raw.reshape(15, 15, heads).transpose(0, 2, 1).transpose(1, 0, 2).astype(np.float32)
     wins = sorted(set(list(range((nwh - 1) * nww, nw)) + list(range(nww - 1, nw, nww)) +
@@ -124,7 +129,7 @@ def test_attention_operator_sweep_config5(be, owt, level):
         assert np.isfinite(got).all()
         ref = _attn_windows_f64(qkv, rp, nwh, nww, c, heads, shift, wins)
         worst = max(float(np.abs(got[wi * 64:(wi + 1) * 64] - ref[wi]).max()) for wi in wins)
-        assert worst <= 2e-5, (level, shift, worst)
+        assert worst <= 2e-5, (level, shift, hard, worst)
 
 
 def test_1080p_properties(be):
