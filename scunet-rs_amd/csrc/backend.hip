@@ -731,6 +731,10 @@ extern "C" {
 
 const char* scunet_hip_create_error(void) { return g_create_error.c_str(); }
 
+static int create_handle(const char* path, scunet_hip** out);
+
+// No C++ exception leaves the C ABI: a failed host allocation while reading or repacking the
+// checkpoint is reported like any other create error.
 int scunet_hip_create(const char* path, scunet_hip** out) {
     g_create_error.clear();
     if (!out) {
@@ -738,6 +742,15 @@ int scunet_hip_create(const char* path, scunet_hip** out) {
         return 1;
     }
     *out = nullptr;
+    try {
+        return create_handle(path, out);
+    } catch (const std::exception& e) {
+        g_create_error = std::string("scunet_hip_create: ") + e.what();
+        return 1;
+    }
+}
+
+static int create_handle(const char* path, scunet_hip** out) {
     std::unique_ptr<scunet_hip> h(new scunet_hip());
     std::string err;
     if (!h->wt.load(path ? path : "", &err)) {
@@ -788,7 +801,12 @@ int scunet_hip_set_precision(scunet_hip* h, int mode) {
         fail(h, "scunet_hip_set_precision: mode must be SCUNET_HIP_FP32 (0) or SCUNET_HIP_FP16 (1)");
         return 1;
     }
-    if (mode == SCUNET_HIP_FP16 && !build_h16_weights(h)) return 1;
+    try {
+        if (mode == SCUNET_HIP_FP16 && !build_h16_weights(h)) return 1;
+    } catch (const std::exception& e) {
+        fail(h, std::string("scunet_hip_set_precision: ") + e.what());
+        return 1;
+    }
     h->h16 = mode;
     return 0;
 }
@@ -891,9 +909,13 @@ int scunet_hip_run_batch(scunet_hip* h, const float* x, size_t nimg, size_t c, s
 int scunet_hip_device_need(const scunet_hip* h, size_t c, size_t hh, size_t ww, int host_io, size_t* scratch_bytes,
                            size_t* more_bytes) {
     if (!h || hh == 0 || ww == 0) return 1;
-    const auto need = arena_need(h, arena_plan(h, pad64(hh), pad64(ww), host_io ? c * hh * ww : 0, false));
-    if (scratch_bytes) *scratch_bytes = need.first;
-    if (more_bytes) *more_bytes = need.second;
+    try {
+        const auto need = arena_need(h, arena_plan(h, pad64(hh), pad64(ww), host_io ? c * hh * ww : 0, false));
+        if (scratch_bytes) *scratch_bytes = need.first;
+        if (more_bytes) *more_bytes = need.second;
+    } catch (const std::exception&) {
+        return 1;
+    }
     return 0;
 }
 

@@ -14,6 +14,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <new>
 #include <string>
 #include <vector>
 
@@ -158,7 +159,15 @@ int main(int argc, char** argv) {
     if (!a.quiet) std::fprintf(stderr, "scunet: device hip%s\n", a.fp16 ? " (fp16 operands)" : "");
 
     auto t0 = std::chrono::steady_clock::now();
-    std::vector<float> y(c * hh * ww);
+    std::vector<float> y;
+    try {
+        y.resize(c * hh * ww);
+    } catch (const std::bad_alloc&) {
+        std::fprintf(stderr, "scunet: out of host memory for a %zux%zu image\n", ww, hh);
+        scunet_image_free(x);
+        scunet_hip_destroy(h);
+        return 1;
+    }
     int rc = scunet_hip_run(h, x, c, hh, ww, y.data());
     scunet_image_free(x);
     if (rc != 0) {

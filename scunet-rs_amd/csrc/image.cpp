@@ -16,6 +16,8 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <new>
+#include <stdexcept>
 #include <string>
 #include <vector>
 
@@ -172,7 +174,10 @@ int decode(const std::string& path, float** data, size_t* oc, size_t* oh, size_t
         return fail(path + ": " + std::to_string(depth) + "-bit samples; this reader takes 8-bit PNGs only");
     if (!have_iend) return fail(path + ": truncated PNG (no IEND)");
     if (idat.empty()) return fail(path + ": no image data (IDAT)");
-    if (uint64_t(w) * h > (uint64_t(1) << 34)) return fail(path + ": image too large");
+    // 2^28 pixels: beyond what the network can run on one device (about 1.6 KB of device
+    // memory per pixel), and a bound on what a header can make this reader allocate.
+    if (uint64_t(w) * h > (uint64_t(1) << 28))
+        return fail(path + ": image too large (" + std::to_string(w) + "x" + std::to_string(h) + ")");
 
     // The passes' geometry and the size of the filtered stream.
     struct Pass { size_t x0, y0, dx, dy, pw, ph; };
@@ -188,6 +193,11 @@ int decode(const std::string& path, float** data, size_t* oc, size_t* oh, size_t
     }
     size_t raw_n = 0;
     for (auto& p : passes) raw_n += p.ph * (1 + p.pw * spp);
+    // deflate expands at most ~1032:1, so a stream this short cannot fill the image: refuse
+    // before allocating for it.
+    if (idat.size() * 1032 + 64 < raw_n)
+        return fail(path + ": image data ends early (" + std::to_string(idat.size()) +
+                    " compressed bytes for " + std::to_string(raw_n) + ")");
     std::vector<uint8_t> raw(raw_n);
 
     z_stream z;
@@ -326,11 +336,19 @@ int encode(const std::string& path, const float* data, size_t c, size_t h, size_
 
 extern "C" {
 
+// No C++ exception leaves the C ABI: an allocation that fails (a header claiming a huge
+// image, say) is reported like any other error.
 int scunet_image_read(const char* path, float** data, size_t* c, size_t* h, size_t* w) {
     g_err.clear();
     if (!path || !data || !c || !h || !w) return fail("scunet_image_read: null argument");
     *data = nullptr;
-    return decode(path, data, c, h, w);
+    try {
+        return decode(path, data, c, h, w);
+    } catch (const std::bad_alloc&) {
+        return fail(std::string(path) + ": out of host memory");
+    } catch (const std::exception& e) {
+        return fail(std::string(path) + ": " + e.what());
+    }
 }
 
 void scunet_image_free(float* data) { std::free(data); }
@@ -338,7 +356,13 @@ void scunet_image_free(float* data) { std::free(data); }
 int scunet_image_write(const char* path, const float* data, size_t c, size_t h, size_t w) {
     g_err.clear();
     if (!path || !data) return fail("scunet_image_write: null argument");
-    return encode(path, data, c, h, w);
+    try {
+        return encode(path, data, c, h, w);
+    } catch (const std::bad_alloc&) {
+        return fail(std::string(path) + ": out of host memory");
+    } catch (const std::exception& e) {
+        return fail(std::string(path) + ": " + e.what());
+    }
 }
 
 const char* scunet_image_error(void) { return g_err.c_str(); }

@@ -245,6 +245,13 @@ def test_malformed_files_are_named(tmp_path):
             _chunk(b"IEND", b""))
     with pytest.raises(image.ImageError, match="image data ends early"):
         image.read(_write(tmp_path, "short.png", blob))
+    # A header claiming a huge image is refused before anything is allocated for it.
+    for (w, h), msg in [((1 << 15, 1 << 14), "image too large"), ((8000, 8000), "image data ends early")]:
+        ihdr = struct.pack(">IIBBBBB", w, h, 8, 2, 0, 0, 0)
+        blob = (b"\x89PNG\r\n\x1a\n" + _chunk(b"IHDR", ihdr) + _chunk(b"IDAT", zlib.compress(bytes(64))) +
+                _chunk(b"IEND", b""))
+        with pytest.raises(image.ImageError, match=msg):
+            image.read(_write(tmp_path, "huge.png", blob))
     with pytest.raises(image.ImageError, match="No such file"):
         image.read(tmp_path / "missing.png")
     with pytest.raises(image.ImageError, match="cannot write 2 channels as PNG"):
