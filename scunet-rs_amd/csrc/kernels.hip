@@ -1420,13 +1420,16 @@ struct WinoUnit {
     int y0, x0, co0;
 };
 DEVI WinoUnit wino_unit(long u, int tx, int nb, long tiles, int cbw = 16) {
-    // u = 8 j + xcd; within an XCD, consecutive j walk the cout blocks of one tile.
-    const long xcd = u & 7, j = u >> 3;
-    const long sp = (j / nb) * 8 + xcd;
+    // u = 8 j + xcd; within an XCD, consecutive j walk the cout blocks of one tile. Unit and
+    // tile indices fit 32 bits (the launcher bounds the plane below 2^32 elements), so the
+    // divisions are 32-bit.
+    const unsigned uu = unsigned(u), xcd = uu & 7u, j = uu >> 3;
+    const unsigned q = j / unsigned(nb), sp = q * 8u + xcd;
     WinoUnit w;
-    w.co0 = int(j % nb) * cbw;
-    w.y0 = sp < tiles ? int(sp / tx) * 16 : -1;
-    w.x0 = int(sp % tx) * 16;
+    w.co0 = int(j - q * unsigned(nb)) * cbw;
+    const unsigned ty = sp / unsigned(tx);
+    w.y0 = long(sp) < tiles ? int(ty) * 16 : -1;
+    w.x0 = int(sp - ty * unsigned(tx)) * 16;
     return w;
 }
 
@@ -1666,8 +1669,11 @@ __global__ __launch_bounds__(512) void k_wino2(Conv3Args a, long tiles, long uni
     // acc[cb][ii][j]: M[2hh + ii][j] for channel block cb (co0 + 16 cb + 4lg .. +3).
     f4 acc[2][2][4];
     // One slice: the two rows of V = B^T d B this half owns, then 2 x 4 x 2 x 4 products.
-    auto slice = [&](auto HHc, const float* buf, int ci0, bool mrow) {
+    // FIRST: the unit's first slice starts the sums (zero accumulator operand), so the
+    // accumulators are never cleared with separate moves.
+    auto slice = [&](auto HHc, auto FIRSTc, const float* buf, int ci0, bool mrow) {
         constexpr int H2 = decltype(HHc)::value;
+        constexpr bool FIRST = decltype(FIRSTc)::value;
         const float* Us = buf + HSZ;
         f4 t[2][4];
 #pragma unroll
@@ -1704,7 +1710,9 @@ __global__ __launch_bounds__(512) void k_wino2(Conv3Args a, long tiles, long uni
                     else
                         uu = ld4(&Us[ur * LDU + lg * 4]);
 #pragma unroll
-                    for (int s4 = 0; s4 < 4; ++s4) acc[cb][ii][j] = mfma4(uu[s4], v[j][s4], acc[cb][ii][j]);
+                    for (int s4 = 0; s4 < 4; ++s4)
+                        acc[cb][ii][j] = mfma4(uu[s4], v[j][s4],
+                                               (FIRST && s4 == 0) ? f4{0.f, 0.f, 0.f, 0.f} : acc[cb][ii][j]);
                 }
         }
     };
@@ -1751,7 +1759,8 @@ __global__ __launch_bounds__(512) void k_wino2(Conv3Args a, long tiles, long uni
                 const int y = w.y0 + 2 * tr + a0, x = w.x0 + 2 * tc + b;
                 if (y >= a.H || x >= a.W) continue;
                 f4 v = yp[H2][a0][b] + ld4(xi + (a0 * 2 + b) * 4);
-                float* o = a.out + (long(y) * a.W + x) * a.ldo + co;
+                // 32-bit element offsets (the launcher bounds the plane below 2^32 elements).
+                float* o = a.out + ((unsigned(y) * unsigned(a.W) + unsigned(x)) * unsigned(a.ldo) + unsigned(co));
                 if constexpr (RELU) {
 #pragma unroll
                     for (int q = 0; q < 4; ++q) v[q] = fmaxf(v[q], 0.0f);
@@ -1770,7 +1779,8 @@ __global__ __launch_bounds__(512) void k_wino2(Conv3Args a, long tiles, long uni
             for (int b = 0; b < 2; ++b) {
                 const int y = w.y0 + 2 * tr + a0, x = w.x0 + 2 * tc + b;
                 res[a0][b] = (w.y0 >= 0 && y < a.H && x < a.W)
-                                 ? ld4(a.out + (long(y) * a.W + x) * a.ldo + w.co0 + hh * 16 + lg * 4)
+                                 ? ld4(a.out + ((unsigned(y) * unsigned(a.W) + unsigned(x)) * unsigned(a.ldo) +
+                                                unsigned(w.co0 + hh * 16 + lg * 4)))
                                  : f4{0.f, 0.f, 0.f, 0.f};
             }
     };
@@ -1793,12 +1803,6 @@ __global__ __launch_bounds__(512) void k_wino2(Conv3Args a, long tiles, long uni
     __syncthreads();
     int kb = 0;                              // buffer of the current slice
     for (;;) {
-#pragma unroll
-        for (int cb = 0; cb < 2; ++cb)
-#pragma unroll
-            for (int ii = 0; ii < 2; ++ii)
-#pragma unroll
-                for (int j = 0; j < 4; ++j) acc[cb][ii][j] = f4{0.f, 0.f, 0.f, 0.f};
         const long un = u + gridDim.x;
         const WinoUnit nxt = wino_unit(un, tx, nb, tiles, CB);
         halo_offsets(nxt, hnxt);
@@ -1819,8 +1823,17 @@ __global__ __launch_bounds__(512) void k_wino2(Conv3Args a, long tiles, long uni
                 const int yo = cur.y0 + 2 * tr;
                 mrow = hh == 0 ? yo % a.img_h == 0 : (yo + 2) % a.img_h == 0;
             }
-            if (hh == 0) slice(std::integral_constant<int, 0>{}, buf, c * BK, mrow);
-            else slice(std::integral_constant<int, 1>{}, buf, c * BK, mrow);
+            using I0 = std::integral_constant<int, 0>;
+            using I1 = std::integral_constant<int, 1>;
+            using T1 = std::integral_constant<bool, true>;
+            using T0 = std::integral_constant<bool, false>;
+            if (c == 0) {
+                if (hh == 0) slice(I0{}, T1{}, buf, c * BK, mrow);
+                else slice(I1{}, T1{}, buf, c * BK, mrow);
+            } else {
+                if (hh == 0) slice(I0{}, T0{}, buf, c * BK, mrow);
+                else slice(I1{}, T0{}, buf, c * BK, mrow);
+            }
             if (more) stash(lds + (kb ^ 1) * BSZ);
             __syncthreads();
             kb ^= 1;
@@ -1884,7 +1897,8 @@ bool conv3x3_winograd(const Conv3Args& a, bool relu, hipStream_t s, const char**
         *why = "conv3x3_winograd: cin and cout must be multiples of 16 and the plane even";
         return false;
     }
-    if (double(a.H) * a.W * a.ldi >= 4294967296.0 || double(a.cout) * a.cin * 16 >= 4294967296.0) {
+    if (double(a.H) * a.W * a.ldi >= 4294967296.0 || double(a.H) * a.W * a.ldo >= 4294967296.0 ||
+        double(a.cout) * a.cin * 16 >= 4294967296.0) {
         *why = "conv3x3_winograd: plane too large for 32-bit element offsets";
         return false;
     }
