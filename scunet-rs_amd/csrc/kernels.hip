@@ -473,11 +473,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const long mtiles = (g.M + 64 * MT - 1) / (64 * MT);
     const long G = gridDim.x;
     // Rows of this wave in tile t (g.M when the tile is past the end: no loads, no stores).
+    // Tile indices fit 32 bits (fewer than 2^31 tiles), so the divisions are 32-bit.
     auto decode = [&](long t, long& m0, int& n0) {
-        const long xcd = t & 7, j = t >> 3;
-        const long mt = (j / ntn) * 8 + xcd;
-        n0 = int(j % ntn) * BN;
-        m0 = mt < mtiles ? mt * 64 * MT + wave * 16 * MT : g.M;
+        const unsigned tt = unsigned(t), xcd = tt & 7u, j = tt >> 3;
+        const unsigned q = j / unsigned(ntn), mt = q * 8u + xcd;
+        n0 = int(j - q * unsigned(ntn)) * BN;
+        m0 = long(mt) < mtiles ? long(mt) * 64 * MT + wave * 16 * MT : g.M;
     };
     auto a_get = [&](long row, int k) -> f4 {
         if (row >= g.M) return f4{0.f, 0.f, 0.f, 0.f};
@@ -695,6 +696,8 @@ static void launch_gemm3_h16(const GemmArgs& g, GemmA a, GemmE e, hipStream_t s)
 }
 
 static bool launch_gemm3(const GemmArgs& g, GemmA a, GemmE e, hipStream_t s) {
+    // k_gemm3 decodes tile indices in 32 bits (at most 2^31 tiles of 16 rows or more).
+    if (g.M / 16 >= (1L << 31)) return false;
     if (g.W16 && a != A_LN && g.K % 32 == 0 && g.N % 64 == 0) {
         // The level-0 down-conv (N = 128) reads its patches once with a 128-wide N block:
         // 382 -> 268 us per launch; the other shapes measured best as below.
@@ -2107,9 +2110,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     const long u = long(blockIdx.x) * 4 + wave;
     if (u >= units) return;                      // whole wave exits together
     const int li = lane & 15, lg = lane >> 4;
-    const long wi = u / a.heads;
-    const int h = int(u - wi * a.heads);
-    const int wh = int(wi / a.nww), ww = int(wi - long(wh) * a.nww);
+    // (window, head) and window indices fit 32 bits (the launch grid is 32-bit).
+    const unsigned wi = unsigned(u) / unsigned(a.heads);
+    const int h = int(unsigned(u) - wi * unsigned(a.heads));
+    const int wh = int(wi / unsigned(a.nww)), ww = int(wi - unsigned(wh) * unsigned(a.nww));
     const int hoff = h * 32;
 
     // Element offsets of the rows of tokens 16m + li (Q, K, V and the output). In pixel
@@ -2296,10 +2300,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(T == 32 ? 2
     const long wi = long(blockIdx.x) * 4 + wave;
     const bool valid = wi < nw;
     // Window wi = (image, window row, window column); the roll wraps within the image.
-    const int wpi = a.nwh * a.nww;
-    const int img = valid ? int(wi / wpi) : 0;
-    const int wr = valid ? int(wi - long(img) * wpi) : 0;
-    const int wh = wr / a.nww, ww = wr - wh * a.nww;
+    // Window counts fit 32 bits (the launch grid is 32-bit), so the divisions are 32-bit.
+    const unsigned wpi = unsigned(a.nwh) * unsigned(a.nww);
+    const int img = valid ? int(unsigned(wi) / wpi) : 0;
+    const int wr = valid ? int(unsigned(wi) - unsigned(img) * wpi) : 0;
+    const int wh = int(unsigned(wr) / unsigned(a.nww)), ww = wr - wh * a.nww;
     const long ybase = long(img) * a.H;
     ET* xw = xs + wave * 64 * LDX;
     auto rowof = [&](int t) -> long {
@@ -2682,10 +2687,11 @@ __global__ __launch_bounds__(T * 2) __attribute__((amdgpu_waves_per_eu(2, 2))) v
     const int li = lane & 15, lg = lane >> 4;
     const long wi = blockIdx.x;
     // Window wi = (image, window row, window column); the roll wraps within the image.
-    const int wpi = a.nwh * a.nww;
-    const int img = int(wi / wpi);
-    const int wr = int(wi - long(img) * wpi);
-    const int wh = wr / a.nww, ww = wr - wh * a.nww;
+    // Window counts fit 32 bits (the launch grid is 32-bit), so the divisions are 32-bit.
+    const unsigned wpi = unsigned(a.nwh) * unsigned(a.nww);
+    const int img = int(unsigned(wi) / wpi);
+    const int wr = int(unsigned(wi) - unsigned(img) * wpi);
+    const int wh = int(unsigned(wr) / unsigned(a.nww)), ww = wr - wh * a.nww;
     const long ybase = long(img) * a.H;
     auto rowof = [&](int t) -> long {
         int y = wh * 8 + (t >> 3) + a.shift;
