@@ -3,7 +3,7 @@
 the reference CPU path (the oracle restatement of src/cpu.rs) timed beside it.
 
 A step is one whole-image forward of SCUNet colour (in_nc 3, dim 64, config [4]*7,
-window 8, head_dim 32, seeded random-init fp32 weights) on BASELINE config 3: a
+window 8, head_dim 32, seeded random-init fp32 weights) on benchmark config 3: a
 1x3x1080x1920 seeded noisy image already resident in HBM, replicate-padded to
 1088x1920 and cropped back on the device (scunet_hip_run_device: the backend::run
 contract with pad and crop fused into the first and last convolution).
@@ -81,7 +81,7 @@ def cpu_baseline(weights_path, x, rows):
 
 
 def attention_sweep(be, wpath, iters):
-    """the isolated window-attention core (the reference's kernel boundary,
+    """benchmark config 5: the isolated window-attention core (the reference's kernel boundary,
     qkv -> out, cuda.rs:767-808) at each level's 1920x1088 window grid, W and SW. x ~ N(0,1)
     [nw*64][C]; qkv = x Wqkv^T + b with the level's seeded embedding weights; rel-pos
     tables ~ N(0, 0.02) in upstream's [225][heads] storage, re-viewed to [heads][15][15]."""
@@ -139,7 +139,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         log("bench.py: this build runs one image on one GPU; multi-GPU runs are not part of it "
-            "(see DESIGN.md for how a forward would shard). Use --gpus 1.")
+            "(one image per GPU shards with no communication; one image over several GPUs would "
+            "split into 64-row bands with halo exchange). Use --gpus 1.")
         sys.exit(2)
 
     import numpy as np
@@ -321,7 +322,7 @@ def main():
         "dtype": "f32",
         "data": "synthetic (seeded noisy 1080x1920 texture, sigma 15/255; seeded random-init weights)",
         "config": {"workload": "SCUNet-color whole-image forward, 1x3x1080x1920 replicate-padded to 1088x1920 "
-                               "(BASELINE config 3), device-resident input, pad+crop on device",
+                               "(benchmark config 3), device-resident input, pad+crop on device",
                    "in_nc": 3, "dim": 64, "blocks": [4] * 7, "window": 8, "head_dim": 32,
                    "kernel_events": not args.no_kernel_events},
         "roofline": dominant,

@@ -172,7 +172,7 @@ def weights_file(seed=0, in_nc=3, ln_affine="identity", directory=None, **kw):
 
 
 # ---------------------------------------------------------------------------
-# Inputs
+# Inputs (benchmark configs 1-5)
 # ---------------------------------------------------------------------------
 
 def _clamp01(x):

@@ -70,6 +70,6 @@ def max_abs(want, got):
 
 @pytest.fixture(scope="session")
 def weights_path_gray():
-    """The grayscale variant (in_nc = 1), BASELINE config 4's network."""
+    """The grayscale variant (in_nc = 1), benchmark config 4's network."""
     from scunet_hip import synth
     return synth.weights_file(seed=5, in_nc=1)

@@ -1,4 +1,4 @@
-"""BASELINE's workload configurations on the GPU: the grayscale variant, config 2 at its
+"""The benchmark's workload configurations on the GPU: the grayscale variant, config 2 at its
 full size against the oracle, the isolated attention operator of config 5 at its real
 window counts, the fused and three-launch attention halves against each other, and the
 1080p headline size (config 3): every stage against the oracle, and size-independent
@@ -104,7 +104,7 @@ def _attn_windows_f64(qkv, rp, nwh, nww, c, heads, shift, wins):
 @pytest.mark.parametrize("hard", [False, True])
 @pytest.mark.parametrize("level", [0, 1, 2, 3])
 def test_attention_operator_sweep_config5(be, owt, level, hard):
-    """x ~ N(0,1) [nw][64][C] at the 1920x1088 window grid of each level,
+    """benchmark config 5: x ~ N(0,1) [nw][64][C] at the 1920x1088 window grid of each level,
     qkv from the level's seeded embedding weights, rel-pos tables ~ N(0, 0.02) laid out as
     upstream's [225][heads] then re-viewed; W and SW. Checked against a float64 evaluation on
     every window of the last window row and column (where the mask acts) plus a random set.
@@ -376,7 +376,7 @@ def test_run_batch_fp16_equals_single_runs(weights_path):
 
 
 def test_config4_gray_4096_full_size(weights_path_gray):
-    """BASELINE config 4 at its real size, 1x1x4096x4096 (the size whose unfused hidden
+    """benchmark config 4 at its real size, 1x1x4096x4096 (the size whose unfused hidden
     layer passes 2^31 elements): the whole forward is finite, bit-identical on repeat, and the
     device pad/crop path equals the plain forward (4096 needs no padding). One level-0
     ConvTransBlock over the full 4096^2 plane (64 channels, both window phases) is checked
