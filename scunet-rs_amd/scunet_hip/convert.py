@@ -94,7 +94,9 @@ def convert(src, dst, variant=None, head_dim=32, window=8):
 
 
 def main(argv=None):
-    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap = argparse.ArgumentParser(prog="python -m scunet_hip.convert",
+                                 description="Convert a published SCUNet .pth checkpoint into the "
+                                             "safetensors file this backend and the reference crate load.")
     ap.add_argument("src")
     ap.add_argument("dst")
     ap.add_argument("--variant", default=None)
