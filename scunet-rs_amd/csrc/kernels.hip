@@ -3222,16 +3222,33 @@ __global__ __launch_bounds__(256) void k_tail(const float* __restrict__ in, int 
     float acc[COUT];
 #pragma unroll
     for (int o = 0; o < COUT; ++o) acc[o] = 0.f;
-    for (int c0 = 0; c0 < DIM; c0 += CH) {
-        __syncthreads();
-        for (int f = threadIdx.x; f < HW * HW * 4; f += 256) {
+    // The halo slice for channels c0 .. c0 + 15 (at most 6 float4 per thread), loaded one slice
+    // ahead into registers: slice c0 + 16 reads the other halves of the 128-byte lines slice c0
+    // read, so it is requested while they are still in the caches, and its latency overlaps
+    // the current slice's arithmetic.
+    constexpr int NV = (HW * HW * 4 + 255) / 256;
+    f4 hv[NV];
+    auto hload = [&](int c0) {
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const int f = threadIdx.x + i * 256;
             const int px = f >> 2, c4 = f & 3;
             const int gy = y0 - 1 + px / HW, gx = x0 - 1 + px % HW;
-            f4 v = {0.f, 0.f, 0.f, 0.f};
-            if (gy >= 0 && gy < H && gx >= 0 && gx < W) v = ld4(in + (long(gy) * W + gx) * DIM + c0 + c4 * 4);
-            st4(&hs[px * LDC + c4 * 4], v);
+            hv[i] = (f < HW * HW * 4 && gy >= 0 && gy < H && gx >= 0 && gx < W)
+                        ? ld4(in + (long(gy) * W + gx) * DIM + c0 + c4 * 4)
+                        : f4{0.f, 0.f, 0.f, 0.f};
+        }
+    };
+    hload(0);
+    for (int c0 = 0; c0 < DIM; c0 += CH) {
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const int f = threadIdx.x + i * 256;
+            if (f < HW * HW * 4) st4(&hs[(f >> 2) * LDC + (f & 3) * 4], hv[i]);
         }
         __syncthreads();
+        if (c0 + CH < DIM) hload(c0 + CH);
 #pragma unroll
         for (int c4 = 0; c4 < 4; ++c4) {
             f4 v[9];
