@@ -3153,12 +3153,14 @@ __global__ __launch_bounds__(256) void k_head(const float* __restrict__ x, int c
     for (int nt = 0; nt < 4; ++nt)
 #pragma unroll
         for (int kg = 0; kg < 2; ++kg) wf[nt][kg] = ld4(&sw[(nt * 16 + li) * LDW + kg * 16 + lg * 4]);
-    for (int step = 0; step < 4; ++step) {
+    // The 4 pixel groups of this wave, software-pipelined: the next group's input taps are
+    // requested before the current group's products and stores (and, when accumulating, the
+    // current group's output rows before its products).
+    auto gather = [&](int step, f4 (&av)[2]) {
         const long p = (long(blockIdx.x) * 16 + wave * 4 + step) * 16 + li;
         const int yy = int(p / W), xx = int(p - long(yy) * W);
         const int b = yy / H, y = yy - b * H;
         const float* xb = x + long(b) * cin * hh * ww;
-        f4 av[2];
 #pragma unroll
         for (int kg = 0; kg < 2; ++kg)
 #pragma unroll
@@ -3173,6 +3175,19 @@ __global__ __launch_bounds__(256) void k_head(const float* __restrict__ x, int c
                 }
                 av[kg][s] = v;
             }
+    };
+    f4 cur[2], nxt[2];
+    gather(0, cur);
+#pragma unroll
+    for (int step = 0; step < 4; ++step) {
+        const long p = (long(blockIdx.x) * 16 + wave * 4 + step) * 16 + li;
+        float* o = out + p * 64 + lg * 4;
+        f4 prev[4];
+        if (add && p < P) {
+#pragma unroll
+            for (int nt = 0; nt < 4; ++nt) prev[nt] = ld4(o + nt * 16);
+        }
+        if (step + 1 < 4) gather(step + 1, nxt);
         f4 acc[4];
 #pragma unroll
         for (int nt = 0; nt < 4; ++nt) acc[nt] = f4{0.f, 0.f, 0.f, 0.f};
@@ -3181,12 +3196,13 @@ __global__ __launch_bounds__(256) void k_head(const float* __restrict__ x, int c
 #pragma unroll
             for (int s = 0; s < 4; ++s)
 #pragma unroll
-                for (int nt = 0; nt < 4; ++nt) acc[nt] = mfma4(wf[nt][kg][s], av[kg][s], acc[nt]);
+                for (int nt = 0; nt < 4; ++nt) acc[nt] = mfma4(wf[nt][kg][s], cur[kg][s], acc[nt]);
         if (p < P) {
-            float* o = out + p * 64 + lg * 4;
 #pragma unroll
-            for (int nt = 0; nt < 4; ++nt) st4(o + nt * 16, add ? ld4(o + nt * 16) + acc[nt] : acc[nt]);
+            for (int nt = 0; nt < 4; ++nt) st4(o + nt * 16, add ? prev[nt] + acc[nt] : acc[nt]);
         }
+#pragma unroll
+        for (int kg = 0; kg < 2; ++kg) cur[kg] = nxt[kg];
     }
 }
 
