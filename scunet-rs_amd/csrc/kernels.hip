@@ -2315,14 +2315,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(T == 32 ? 2
         return (ybase + y) * a.W + x;
     };
 
-    // 1. LN1 of the window's tokens into LDS.
+    // 1. LN1 of the window's tokens into LDS. The raw rows stay in registers for the
+    // attention residual (the wave is register-limited to two per SIMD either way).
+    f4 xin[4][KG];
     if (valid) {
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt) {
             const long row = rowof(mt * 16 + li);
             f4 v[KG];
 #pragma unroll
-            for (int kg = 0; kg < KG; ++kg) v[kg] = ld4(a.x + row * a.ldx + kg * 16 + lg * 4);
+            for (int kg = 0; kg < KG; ++kg) xin[mt][kg] = v[kg] = ld4(a.x + row * a.ldx + kg * 16 + lg * 4);
             float sm = 0.f;
 #pragma unroll
             for (int kg = 0; kg < KG; ++kg) sm += (v[kg].x + v[kg].y) + (v[kg].z + v[kg].w);
@@ -2535,12 +2537,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(T == 32 ? 2
     // 3. Residual: lanes hold outputs 16ot + 4lg .. +3 of token 16nt + li.
     f4 xr[4][OT];
 #pragma unroll
-    for (int nt = 0; nt < 4; ++nt) {
-        const long row = rowof(nt * 16 + li);
+    for (int nt = 0; nt < 4; ++nt)
 #pragma unroll
-        for (int ot = 0; ot < OT; ++ot)
-            xr[nt][ot] = ld4(a.x + row * a.ldx + ot * 16 + lg * 4) + (acc[nt][ot] + ld4(a.bp + ot * 16 + lg * 4));
-    }
+        for (int ot = 0; ot < OT; ++ot) xr[nt][ot] = xin[nt][ot] + (acc[nt][ot] + ld4(a.bp + ot * 16 + lg * 4));
     if constexpr (MLP) {
         // 4. The MLP on the window's tokens (cpu.rs:800-860), exactly as k_mlp computes it:
         // LN2 in registers, the hidden layer produced 32 units at a time transposed (so it
