@@ -2096,14 +2096,13 @@ void winograd_filter(const float* g, int cout, int cin, float* u) {
 //   normalisation is applied to the 8 outputs rather than the 16 weights.
 // Logits are kept in log2 units, l = (q.k) * scale * log2(e) + log2(e) * bias, so a logit is
 // one FMA and softmax uses 2^(l - max); masked logits are -FLT_MAX/4 (cpu.rs:365-370,
-// 681-683). The per-head 15x15 bias tables sit in LDS; each lane reads the 28 entries its
-// 64 logits use. V is transposed through a per-wave LDS slice so that every global load is
-// a 16-byte row load.
+// 681-683). The per-head 15x15 bias tables sit in LDS; each lane reads the entries its 64
+// logits use where the logits are formed. V is read transposed straight from memory (4-byte
+// loads, 64 contiguous bytes per key), so the only LDS is the 7.2 KB of tables and the
+// kernel fits in 128 VGPRs: four waves per SIMD, 4 096 (window, head) units in flight.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) void k_attention(AttnArgs a, long units) {
-    constexpr int VP = 72;                        // V^T row pitch (conflict-free b128 reads)
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4))) void k_attention(AttnArgs a, long units) {
     __shared__ float rps[8 * 225];                // log2(e) * rel-pos tables, all heads
-    __shared__ float vts[4][32 * VP];             // per wave: V^T [dim][key]
     for (int i = threadIdx.x; i < a.heads * 225; i += 256) rps[i] = a.tab[i];
     __syncthreads();                              // the only barrier
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -2116,59 +2115,67 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     const int wh = int(wi / unsigned(a.nww)), ww = int(wi - unsigned(wh) * unsigned(a.nww));
     const int hoff = h * 32;
 
-    // Element offsets of the rows of tokens 16m + li (Q, K, V and the output). In pixel
-    // mode token (ty, tx) of window (wh, ww) is pixel ((8wh + ty + shift) mod H,
-    // (8ww + tx + shift) mod W) (cpu.rs:648-652's cyclic shift folded into the
-    // addressing); the launcher checks that every offset fits 32 bits.
-    unsigned off[4];
+    // Element offsets of the rows of tokens 16m + li (Q and K: 16-byte row loads), and the
+    // row and column parts of tokens 16kt + 4lg + r (V, read transposed: lane li takes dim
+    // 16nd + li of those 4 keys with 4-byte loads, 64 contiguous bytes per key and
+    // instruction). In pixel mode token (ty, tx) of window (wh, ww) is pixel
+    // ((8wh + ty + shift) mod H, (8ww + tx + shift) mod W) (cpu.rs:648-652's cyclic shift
+    // folded into the addressing); the launcher checks that every offset fits 32 bits.
+    unsigned off[4], vy[4], vx[4];
     if (a.pixel_mode) {
         auto wy = [&](int ty) { int y = wh * 8 + ty + a.shift; return unsigned(y >= a.H ? y - a.H : y); };
-        int x = ww * 8 + (li & 7) + a.shift;
-        const unsigned xq = unsigned(x >= a.W ? x - a.W : x);
+        auto wx = [&](int tx) { int x = ww * 8 + tx + a.shift; return unsigned(x >= a.W ? x - a.W : x); };
+        const unsigned xq = wx(li & 7);
 #pragma unroll
         for (int m = 0; m < 4; ++m) off[m] = (wy(2 * m + (li >> 3)) * unsigned(a.W) + xq) * unsigned(a.ldq);
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt) vy[kt] = wy(2 * kt + (lg >> 1)) * unsigned(a.W);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) vx[r] = wx(4 * (lg & 1) + r);
     } else {
 #pragma unroll
         for (int m = 0; m < 4; ++m) off[m] = (unsigned(wi) * 64u + 16u * m + li) * unsigned(a.ldq);
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt) vy[kt] = unsigned(wi) * 64u + 16u * kt + 4u * lg;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) vx[r] = r;
     }
+    // Row (pixel or window-major token) of token 16m + li, recomputed where the outputs
+    // are stored so that no register holds it through the products.
+    auto row_of = [&](int m) -> unsigned {
+        if (a.pixel_mode) {
+            int y = wh * 8 + 2 * m + (li >> 3) + a.shift, x = ww * 8 + (li & 7) + a.shift;
+            y = y >= a.H ? y - a.H : y;
+            x = x >= a.W ? x - a.W : x;
+            return unsigned(y) * unsigned(a.W) + unsigned(x);
+        }
+        return unsigned(wi) * 64u + 16u * m + li;
+    };
     const float* q_base = a.qkv + hoff;
     const float* k_base = a.qkv + a.C + hoff;
-    const float* v_base = a.qkv + 2 * a.C + hoff;
+    const float* v_base = a.qkv + 2 * a.C + hoff + li;
 
     // All of the window-head's operands are requested before the first product.
-    // Q / K / V rows: token 16m + li, dim group G (dims 16G + 4lg .. +3).
-    f4 kf[4][2], qf[4][2], vr[4][2];
+    // kf / qf: token 16m + li, dims 16G + 4lg .. +3. vv: the A operand of O^T = V^T P^T,
+    // dim 16nd + li against keys 16kt + 4lg + r.
+    f4 kf[4][2], qf[4][2], vv[4][2];
 #pragma unroll
     for (int m = 0; m < 4; ++m)
 #pragma unroll
         for (int G = 0; G < 2; ++G) {
             kf[m][G] = ld4(k_base + off[m] + G * 16 + lg * 4);
             qf[m][G] = ld4(q_base + off[m] + G * 16 + lg * 4);
-            vr[m][G] = ld4(v_base + off[m] + G * 16 + lg * 4);
         }
-    // Bias: query p = 16nt + li and key q = 16mt + 4lg + r give table entry
-    // (p/8 - q/8 + 7) * 15 + (p%8 - q%8 + 7) = base + 30 (nt - mt) - r (cpu.rs:532-546),
-    // so a lane needs only the 28 entries base + 30 d - r, d = -3 .. 3.
-    const int base = 15 * ((li >> 3) - (lg >> 1)) + (li & 7) - 4 * (lg & 1) + 112;
-    float bl[7][4];
-#pragma unroll
-    for (int d = 0; d < 7; ++d)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) bl[d][r] = rps[h * 225 + base + 30 * (d - 3) - r];
-    // V^T through this wave's LDS slice: written as rows arrive, read back as the A operand
-    // of O^T = V^T P^T (dim 16nd + li, keys 16kt + 4lg .. +3).
-    float* vt = vts[wave];
-#pragma unroll
-    for (int m = 0; m < 4; ++m)
-#pragma unroll
-        for (int G = 0; G < 2; ++G)
-#pragma unroll
-            for (int c = 0; c < 4; ++c) vt[(16 * G + 4 * lg + c) * VP + 16 * m + li] = vr[m][G][c];
-    f4 vv[4][2];
 #pragma unroll
     for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-        for (int nd = 0; nd < 2; ++nd) vv[kt][nd] = ld4(vt + (16 * nd + li) * VP + 16 * kt + 4 * lg);
+        for (int nd = 0; nd < 2; ++nd)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) vv[kt][nd][r] = v_base[(vy[kt] + vx[r]) * unsigned(a.ldq) + 16 * nd];
+    // Bias: query p = 16nt + li and key q = 16mt + 4lg + r give table entry
+    // (p/8 - q/8 + 7) * 15 + (p%8 - q%8 + 7) = base + 30 (nt - mt) - r (cpu.rs:532-546);
+    // read from LDS where each logit is formed.
+    const int base = h * 225 + 15 * ((li >> 3) - (lg >> 1)) + (li & 7) - 4 * (lg & 1) + 112;
 
     // Shifted-window mask (cpu.rs:548-589, 681-683): in the last window row, query and key
     // on different sides of the row split; in the last window column, on different sides of
@@ -2190,12 +2197,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
             for (int s4 = 0; s4 < 4; ++s4)
 #pragma unroll
                 for (int mt = 0; mt < 4; ++mt) S[mt] = mfma4(kf[mt][G][s4], qf[nt][G][s4], S[mt]);
-
         // Logits for query 16nt + li against keys 16mt + 4lg + r.
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) S[mt][r] = fmaf(S[mt][r], sc, bl[nt - mt + 3][r]);
+            for (int r = 0; r < 4; ++r) S[mt][r] = fmaf(S[mt][r], sc, rps[base + 30 * (nt - mt) - r]);
         if (row_edge || col_edge) {
 #pragma unroll
             for (int mt = 0; mt < 4; ++mt) {
@@ -2222,7 +2228,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
             }
         sum += __shfl_xor(sum, 16);
         sum += __shfl_xor(sum, 32);
-
         // O^T = V^T P^T with the unnormalised weights (lane = query, registers = 4
         // consecutive keys: the B operand as they stand), then O / sum: each lane ends with
         // dims 16nd + 4lg .. +3 of query 16nt + li.
@@ -2234,7 +2239,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
 #pragma unroll
                 for (int nd = 0; nd < 2; ++nd) O[nd] = mfma4(vv[kt][nd][r], S[kt][r], O[nd]);
         const float inv = 1.0f / sum;
-        float* o = a.out + long(off[nt] / unsigned(a.ldq)) * a.ldo + hoff + lg * 4;
+        float* o = a.out + long(row_of(nt)) * a.ldo + hoff + lg * 4;
         st4(o, O[0] * inv);
         st4(o + 16, O[1] * inv);
     }
