@@ -761,9 +761,11 @@ static bool launch_gemm2(const GemmArgs& g, GemmA a, GemmE e, hipStream_t s) {
     // Measured on the 1080p forward: for N <= 128, 64-wide N blocks and 32-row waves (more
     // waves per SIMD) beat wider tiles; above, 128-wide blocks.
     // The up-conv (skip-sum operand, depth-to-space epilogue): one 16-row tile per wave, at
-    // four waves per SIMD (530 -> 480 us at level 0, 430 -> 400 us at level 1).
+    // four waves per SIMD (530 -> 480 us at level 0, 430 -> 400 us at level 1), and 16-wide
+    // K slices (half the LDS per workgroup: 481 -> 456, 398 -> 380 and 370 -> 354 us at
+    // levels 0, 1 and 2; the persistent GEMMs measured slower with them).
     if (a == A_ADD2 && g.N % 128 == 0) {
-        launch_gemm2_a<1, 128, 32>(g, a, e, s);
+        launch_gemm2_a<1, 128, 16>(g, a, e, s);
         return true;
     }
     if (g.N % 64 == 0 && g.N <= 128) launch_gemm2_a<2, 64, 32>(g, a, e, s);
