@@ -62,6 +62,7 @@ struct scunet_hip {
     bool unfused_msa = false;            // route every level through the 3-launch attention half
     bool direct3x3 = false;              // the direct implicit-GEMM 3x3 instead of Winograd
     bool wino16 = false;                 // Winograd with 16 output channels per unit only
+    bool wino_pair = false;              // 16-channel Winograd always in 8 x 16 pair units
     bool gemm2 = false;                  // one tile per workgroup GEMM (no persistent walker)
     bool gemm1x1 = false;                // the tiled GEMM for every 1x1 (no resident weights, no chaining)
     bool separate_mlp = false;           // the MLP as its own kernel also at t = 32
@@ -332,6 +333,7 @@ bool run_conv3(scunet_hip* h, const std::string& name, Conv3Args c, bool relu) {
     } else if (!h->direct3x3 && u && c.cin % 16 == 0 && c.cout % 16 == 0 && c.H % 2 == 0 && c.W % 2 == 0) {
         c.w = u;
         c.cblock = h->wino16 ? 16 : 0;
+        c.pair = h->wino_pair ? 1 : 0;
         if (!conv3x3_winograd(c, relu, h->stream, &why)) return fail(h, why);
     } else {
         c.w = W(h, name + ".weight");
@@ -778,6 +780,8 @@ static int create_handle(const char* path, scunet_hip** out) {
     // A/B switch: the direct implicit-GEMM 3x3 kernel instead of Winograd F(2x2,3x3).
     h->direct3x3 = std::getenv("SCUNET_HIP_DIRECT3X3") != nullptr;
     h->wino16 = std::getenv("SCUNET_HIP_WINO16") != nullptr;
+    // A/B switch: 16-channel Winograd units always as pairs of 8 x 16 half-tiles.
+    h->wino_pair = std::getenv("SCUNET_HIP_WINO_PAIR") != nullptr;
     h->gemm2 = std::getenv("SCUNET_HIP_GEMM2") != nullptr;
     h->gemm1x1 = std::getenv("SCUNET_HIP_GEMM1X1") != nullptr;
     h->separate_mlp = std::getenv("SCUNET_HIP_SEPARATE_MLP") != nullptr;

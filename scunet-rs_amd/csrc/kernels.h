@@ -122,6 +122,7 @@ struct Conv3Args {
     int H = 0, W = 0, cin = 0, cout = 0;
     int img_h = 0;                 // rows per image (0: the whole plane is one image)
     int cblock = 0;                // Winograd: output channels per unit (0 = 32 below 256 input channels, else 16; 16)
+    int pair = 0;                  // Winograd, 16-channel units: 0 = 8 x 16 pair units when they take fewer rounds, 1 = always
     const half_t* w16 = nullptr;   // fp16 mode: [9][cout][cin] k-permuted (conv3x3_h16)
 };
 // relu=true: out = relu(conv); relu=false: out += conv (the conv half's residual).

@@ -1423,6 +1423,7 @@ bool conv3x3(const Conv3Args& a, bool relu, hipStream_t s, const char** why) {
 // ---------------------------------------------------------------------------
 struct WinoUnit {
     int y0, x0, co0;
+    int y1 = -1, x1 = 0;   // pair units: the second 8 x 16 region (y1 = -1: none)
 };
 DEVI WinoUnit wino_unit(long u, int tx, int nb, long tiles, int cbw = 16) {
     // u = 8 j + xcd; within an XCD, consecutive j walk the cout blocks of one tile. Unit and
@@ -1438,22 +1439,53 @@ DEVI WinoUnit wino_unit(long u, int tx, int nb, long tiles, int cbw = 16) {
     return w;
 }
 
-template <bool RELU, bool BATCH>
+// Pair units (PAIR): the plane is cut into 8 x 16-pixel half-tiles, and a unit is the
+// half-tiles 2p and 2p + 1 of the row-major order (any two; waves 0-1 take the first, waves
+// 2-3 the second) x 16 output channels: the same arithmetic per lane, with twice as many
+// units of half the height. A 136-row plane (the 1/8 level of 1088 rows) then has no
+// half-empty tile row, and 4 080 half-tiles x 16 channel blocks make 2 040 units: 3.98
+// rounds of 512 workgroups instead of 2 160 units in 4.22 (run as 5).
+DEVI WinoUnit wino_pair(long u, int tx, int nb, long pairs, long halfs) {
+    const unsigned uu = unsigned(u), xcd = uu & 7u, j = uu >> 3;
+    const unsigned q = j / unsigned(nb), sp = q * 8u + xcd;
+    WinoUnit w;
+    w.co0 = int(j - q * unsigned(nb)) * 16;
+    const unsigned h0 = 2u * sp, h1 = h0 + 1u;
+    const unsigned r0 = h0 / unsigned(tx), r1 = h1 / unsigned(tx);
+    w.y0 = long(h0) < halfs ? int(r0) * 8 : -1;
+    w.x0 = int(h0 - r0 * unsigned(tx)) * 16;
+    w.y1 = long(h1) < halfs ? int(r1) * 8 : -1;
+    w.x1 = int(h1 - r1 * unsigned(tx)) * 16;
+    (void)pairs;
+    return w;
+}
+
+template <bool RELU, bool BATCH, bool PAIR>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_wino(Conv3Args a, long tiles,
                                                                                          long units) {
     // Halo pixel (py, px) at Hs[(py * HP + px) * LDC]: 5 slots per pixel and 24-pixel rows
     // make the patch reads (lanes 2 pixels apart along a row, two tile rows 2 pixel rows
     // apart) hit 32 distinct slots mod 32 per half-wave; U rows are 24 floats apart.
+    // Pair units keep their two 10 x 18 halos as LDS rows 0-9 and 10-19.
     constexpr int BK = 16, LDC = BK + 4, HW = 18, HP = 24, LDU = BK + 8;
-    constexpr int HV = (HW * HW * 4 + 255) / 256;   // halo float4 per thread
-    constexpr int UV = 16 * 16 * 4 / 256;           // U float4 per thread
-    __shared__ float Hs[HW * HP * LDC];
+    constexpr int HROWS = PAIR ? 20 : HW;            // halo rows in LDS
+    constexpr int HPX = PAIR ? 2 * 10 * HW : HW * HW; // halo pixels per unit
+    constexpr int HV = (HPX * 4 + 255) / 256;        // halo float4 per thread
+    constexpr int UV = 16 * 16 * 4 / 256;            // U float4 per thread
+    __shared__ float Hs[HROWS * HP * LDC];
     __shared__ float Us[16 * 16 * LDU];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int li = lane & 15, lg = lane >> 4;
     const int tx = (a.W + 15) >> 4, nb = a.cout / 16, nch = a.cin / BK;
-    const int tr = 2 * wave + (li >> 3), tc = li & 7;
+    // The wave's tile row within its region and the region's first LDS halo row.
+    const int tr = PAIR ? 2 * (wave & 1) + (li >> 3) : 2 * wave + (li >> 3), tc = li & 7;
+    const int hrow0 = PAIR ? (wave >> 1) * 10 : 0;
+    const long halfs = PAIR ? long((a.H + 7) >> 3) * tx : 0;
+    auto unit_at = [&](long uu) { return PAIR ? wino_pair(uu, tx, nb, tiles, halfs) : wino_unit(uu, tx, nb, tiles); };
+    // Origin of the wave's output region (y < 0: nothing to compute or store).
+    auto ry0 = [&](const WinoUnit& w) { return PAIR && (wave >> 1) ? w.y1 : w.y0; };
+    auto rx0 = [&](const WinoUnit& w) { return PAIR && (wave >> 1) ? w.x1 : w.x0; };
 
     // Load addressing: 32-bit element offsets per lane, fixed per kernel (U) or per unit
     // (halo); a slice only adds its uniform channel base, so the loop does no address
@@ -1472,8 +1504,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         for (int i = 0; i < HV; ++i) {
             const int f = tid + i * 256;
             const int px = f >> 2, c4 = f & 3;
-            const int gy = w.y0 - 1 + px / HW, gx = w.x0 - 1 + px % HW;
-            const bool ok = f < HW * HW * 4 && w.y0 >= 0 && gy >= 0 && gy < a.H && gx >= 0 && gx < a.W;
+            const bool second = PAIR && px >= 10 * HW;
+            const int pp = second ? px - 10 * HW : px;
+            const int oy = second ? w.y1 : w.y0, ox = second ? w.x1 : w.x0;
+            const int gy = oy - 1 + pp / HW, gx = ox - 1 + pp % HW;
+            const bool ok = f < HPX * 4 && oy >= 0 && gy >= 0 && gy < a.H && gx >= 0 && gx < a.W;
             ho[i] = ok ? (unsigned(gy) * unsigned(a.W) + unsigned(gx)) * unsigned(a.ldi) + unsigned(c4 * 4) : NOFF;
         }
     };
@@ -1490,8 +1525,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
         for (int i = 0; i < HV; ++i) {
             const int f = tid + i * 256;
-            if (f < HW * HW * 4) {
-                const int px = f >> 2;
+            if (f < HPX * 4) {
+                const int px = f >> 2;   // pair units: pixel 180 + p is LDS row 10 + p / 18
                 st4(&Hs[((px / HW) * HP + px % HW) * LDC + (f & 3) * 4], rh[i]);
             }
         }
@@ -1504,7 +1539,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 
     long u = blockIdx.x;
     if (u >= units) return;
-    WinoUnit cur = wino_unit(u, tx, nb, tiles);
+    WinoUnit cur = unit_at(u);
     unsigned hcur[HV], hnxt[HV];
     halo_offsets(cur, hcur);
     load(hcur, cur.co0, 0);
@@ -1513,7 +1548,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
         for (int xi = 0; xi < 16; ++xi) acc[xi] = f4{0.f, 0.f, 0.f, 0.f};
         const long un = u + gridDim.x;
-        const WinoUnit nxt = wino_unit(un, tx, nb, tiles);
+        const WinoUnit nxt = unit_at(un);
         halo_offsets(nxt, hnxt);
         for (int c = 0; c < nch; ++c) {
             __syncthreads();
@@ -1527,14 +1562,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             // that ends it, belongs to the neighbouring image and reads as zero padding.
             bool mtop = false, mbot = false;
             if constexpr (BATCH) {
-                const int yo = cur.y0 + 2 * tr;
+                const int yo = ry0(cur) + 2 * tr;
                 mtop = yo % a.img_h == 0;
                 mbot = (yo + 2) % a.img_h == 0;
             }
             f4 t[4][4];
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const float* col = &Hs[((2 * tr) * HP + 2 * tc + j) * LDC + lg * 4];
+                const float* col = &Hs[((hrow0 + 2 * tr) * HP + 2 * tc + j) * LDC + lg * 4];
                 f4 d0 = ld4(col), d1 = ld4(col + HP * LDC), d2 = ld4(col + 2 * HP * LDC),
                    d3 = ld4(col + 3 * HP * LDC);
                 if constexpr (BATCH) {
@@ -1558,7 +1593,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             }
         }
         // Output transform: lane holds M[xi] for its tile, channels co0 + 4lg .. +3.
-        if (cur.y0 >= 0) {
+        if (ry0(cur) >= 0) {
             f4 s0[4], s1[4];
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
@@ -1574,7 +1609,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             for (int i = 0; i < 2; ++i)
 #pragma unroll
                 for (int j = 0; j < 2; ++j) {
-                    const int y = cur.y0 + 2 * tr + i, x = cur.x0 + 2 * tc + j;
+                    const int y = ry0(cur) + 2 * tr + i, x = rx0(cur) + 2 * tc + j;
                     if (y >= a.H || x >= a.W) continue;
                     float* o = a.out + (long(y) * a.W + x) * a.ldo + cur.co0 + lg * 4;
                     f4 v = yv[i][j];
@@ -1862,37 +1897,53 @@ __global__ __launch_bounds__(512) void k_wino2(Conv3Args a, long tiles, long uni
 
 template <bool BATCH>
 static bool launch_wino(const Conv3Args& a, bool relu, bool wide, bool ures, hipStream_t s, const char** why) {
-    static std::atomic<int> cus_c[6] = {}, pc_c[6] = {};
-    const int v = (relu ? 1 : 0) + (ures ? 4 : wide ? 2 : 0);
-    void (*kern)(Conv3Args, long, long) =
-        ures ? (relu ? k_wino2<true, true, BATCH> : k_wino2<false, true, BATCH>)
-             : wide ? (relu ? k_wino2<true, false, BATCH> : k_wino2<false, false, BATCH>)
-                    : (relu ? k_wino<true, BATCH> : k_wino<false, BATCH>);
-    Occ oc;
-    if (!query_occ(kern, ures || wide ? 512 : 256, cus_c[v], pc_c[v], &oc)) {
+    static std::atomic<int> cus_c[8] = {}, pc_c[8] = {};
+    auto occ = [&](int v, void (*kern)(Conv3Args, long, long), int threads, Occ* oc) {
+        if (query_occ(kern, threads, cus_c[v], pc_c[v], oc)) return true;
         *why = "conv3x3_winograd: device query failed";
         return false;
-    }
-    const int cus = oc.cus, pc = oc.per_cu;
-    const long tiles = long((a.W + 15) / 16) * ((a.H + 15) / 16);
+    };
     const int nb = a.cout / (wide ? 32 : 16);
+    const long tiles = long((a.W + 15) / 16) * ((a.H + 15) / 16);
     // Units are numbered 8 j + xcd with j < ceil(tiles / 8) * nb; numbers whose tile is
     // past the end (the last partial group of 8) carry y0 = -1 and do no loads or stores.
     const long units = ((tiles + 7) / 8) * 8 * nb;
-    const long grid = std::min<long>(units, long(cus) * pc);
-    dim3 g{unsigned(grid), 1u, 1u};
+    if (!ures && !wide) {
+        // 16-channel units: 16 x 16 tiles, or pairs of 8 x 16 half-tiles when those take
+        // fewer rounds of the persistent grid (or when a.pair asks for them).
+        Occ o16, op;
+        if (!occ(relu ? 1 : 0, relu ? k_wino<true, BATCH, false> : k_wino<false, BATCH, false>, 256, &o16) ||
+            !occ(relu ? 7 : 6, relu ? k_wino<true, BATCH, true> : k_wino<false, BATCH, true>, 256, &op))
+            return false;
+        const long pairs = (long((a.W + 15) / 16) * ((a.H + 7) / 8) + 1) / 2;
+        const long punits = ((pairs + 7) / 8) * 8 * nb;
+        const long g16 = std::min<long>(units, long(o16.cus) * o16.per_cu);
+        const long gp = std::min<long>(punits, long(op.cus) * op.per_cu);
+        const bool pair = a.pair == 1 || (punits + gp - 1) / gp < (units + g16 - 1) / g16;
+        dim3 g{unsigned(pair ? gp : g16), 1u, 1u}, block{256u, 1u, 1u};
+        if (pair) {
+            if (relu) hipLaunchKernelGGL((k_wino<true, BATCH, true>), g, block, 0, s, a, pairs, punits);
+            else hipLaunchKernelGGL((k_wino<false, BATCH, true>), g, block, 0, s, a, pairs, punits);
+        } else {
+            if (relu) hipLaunchKernelGGL((k_wino<true, BATCH, false>), g, block, 0, s, a, tiles, units);
+            else hipLaunchKernelGGL((k_wino<false, BATCH, false>), g, block, 0, s, a, tiles, units);
+        }
+        return true;
+    }
+    const int v = (relu ? 1 : 0) + (ures ? 4 : 2);
+    Occ oc;
+    if (!occ(v, ures ? (relu ? k_wino2<true, true, BATCH> : k_wino2<false, true, BATCH>)
+                     : (relu ? k_wino2<true, false, BATCH> : k_wino2<false, false, BATCH>),
+             512, &oc))
+        return false;
+    const long grid = std::min<long>(units, long(oc.cus) * oc.per_cu);
+    dim3 g{unsigned(grid), 1u, 1u}, block{512u, 1u, 1u};
     if (ures) {
-        dim3 block{512u, 1u, 1u};
         if (relu) hipLaunchKernelGGL((k_wino2<true, true, BATCH>), g, block, 0, s, a, tiles, units);
         else hipLaunchKernelGGL((k_wino2<false, true, BATCH>), g, block, 0, s, a, tiles, units);
-    } else if (wide) {
-        dim3 block{512u, 1u, 1u};
+    } else {
         if (relu) hipLaunchKernelGGL((k_wino2<true, false, BATCH>), g, block, 0, s, a, tiles, units);
         else hipLaunchKernelGGL((k_wino2<false, false, BATCH>), g, block, 0, s, a, tiles, units);
-    } else {
-        dim3 block{256u, 1u, 1u};
-        if (relu) hipLaunchKernelGGL((k_wino<true, BATCH>), g, block, 0, s, a, tiles, units);
-        else hipLaunchKernelGGL((k_wino<false, BATCH>), g, block, 0, s, a, tiles, units);
     }
     return true;
 }

@@ -172,23 +172,27 @@ def test_config3_1080p_every_stage_against_cpu(be, owt):
     assert np.array_equal(y[:, :h, :w], be.run_fused(x))
 
 
-def _hip_with(weights_path, env):
+def _hip_with(weights_path, *envs):
     from scunet_hip import Hip
-    os.environ[env] = "1"
+    for env in envs:
+        os.environ[env] = "1"
     try:
         return Hip(weights_path)
     finally:
-        del os.environ[env]
+        for env in envs:
+            del os.environ[env]
 
 
 def test_direct_and_winograd_3x3_agree(weights_path, owt):
     """The conv half's 3x3 convolutions by Winograd F(2x2,3x3) with 32 output channels per
-    unit (the default), with 16 (SCUNET_HIP_WINO16) and by the direct implicit GEMM
-    (SCUNET_HIP_DIRECT3X3): all against the oracle's cpu.rs conv3x3, op by op (planes that
-    end in partial 16x16 tiles included) and in a block."""
+    unit (the default), with 16 (SCUNET_HIP_WINO16), with 16 in pairs of 8x16 half-tiles
+    (SCUNET_HIP_WINO_PAIR) and by the direct implicit GEMM (SCUNET_HIP_DIRECT3X3): all
+    against the oracle's cpu.rs conv3x3, op by op (planes that end in partial tiles and odd
+    half-tile counts included) and in a block."""
     from scunet_hip import Hip, synth
     direct = _hip_with(weights_path, "SCUNET_HIP_DIRECT3X3")
     w16 = _hip_with(weights_path, "SCUNET_HIP_WINO16")
+    pair = _hip_with(weights_path, "SCUNET_HIP_WINO16", "SCUNET_HIP_WINO_PAIR")
     wino = Hip(weights_path)
     try:
         for name, c, h, w in (("m_down1.0.conv_block.0", 32, 40, 24), ("m_down2.1.conv_block.2", 64, 16, 24),
@@ -196,17 +200,18 @@ def test_direct_and_winograd_3x3_agree(weights_path, owt):
                               ("m_up1.2.conv_block.0", 32, 18, 34), ("m_up2.3.conv_block.2", 64, 50, 6)):
             x = synth.seq(c * h * w, 0.37).reshape(c, h, w)
             want = O.conv3x3(x, owt.t[name + ".weight"])
-            for tag, be in (("winograd", wino), ("winograd16", w16), ("direct", direct)):
+            for tag, be in (("winograd", wino), ("winograd16", w16), ("pairs", pair), ("direct", direct)):
                 close(f"{tag} {name} {h}x{w}", want, be.op_probe("conv3x3", name, x, c, c, h, w), 1e-5)
         for prefix, shift in (("m_down1.1", 4), ("m_body.2", 0)):
             c = sum(owt.block_dims(prefix))
             x = synth.seq(c * 24 * 32, 0.61).reshape(c, 24, 32)
             want = O.conv_trans_block(owt, prefix, x, shift)
-            for be in (wino, w16, direct):
+            for be in (wino, w16, pair, direct):
                 assert max_abs(want, be.block_dump(prefix, 24, 32, shift, x)) <= STAGE_TOL
     finally:
         wino.close()
         w16.close()
+        pair.close()
         direct.close()
 
 
@@ -363,6 +368,27 @@ def test_run_batch_equals_single_runs(weights_path, n, h, w):
         ys = be.run_batch(xs)
         for i in range(n):
             assert np.array_equal(ys[i], be.run_fused(xs[i])), i
+
+
+def test_winograd_pairs_batch_and_bits(weights_path):
+    """16-channel Winograd units as pairs of 8x16 half-tiles (SCUNET_HIP_WINO_PAIR, with
+    SCUNET_HIP_WINO16 at every level): five stacked 64-row images (8 rows each at the 1/8
+    level: one half-tile row per image, pairs that straddle images) give each image's own
+    forward bit for bit, and the pairs give the same bits as 16x16 units (the arithmetic per
+    tile is the same)."""
+    from scunet_hip import synth
+    xs = np.stack([synth.noisy_image(30 + i, 3, 64, 64, 25) for i in range(5)])
+    pair = _hip_with(weights_path, "SCUNET_HIP_WINO16", "SCUNET_HIP_WINO_PAIR")
+    w16 = _hip_with(weights_path, "SCUNET_HIP_WINO16")
+    try:
+        ys = pair.run_batch(xs)
+        for i in range(5):
+            y = pair.run_fused(xs[i])
+            assert np.array_equal(ys[i], y), i
+            assert np.array_equal(y, w16.run_fused(xs[i])), i
+    finally:
+        pair.close()
+        w16.close()
 
 
 def test_run_batch_fp16_equals_single_runs(weights_path):
