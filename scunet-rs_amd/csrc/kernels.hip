@@ -1245,11 +1245,13 @@ bool mlp(const MlpArgs& a, hipStream_t s, const char** why) {
         case 32: h16 ? go(k_mlp<32, 4, 64, true>, 256) : go(k_mlp<32, 4, 64, false>, 256); break;
         case 64: h16 ? go(k_mlp<64, 2, 64, true>, 128) : go(k_mlp<64, 2, 64, false>, 128); break;
         // fp16: more rows per workgroup (8 waves at t = 128, 2 row tiles per wave at both), so
-        // each streamed weight slice feeds 256 (t = 128) or 128 (t = 256) rows.
-        case 128: h16 ? go(k_mlp<128, 2, 32, true, 8>, 256, 512) : go(k_mlp<128, 1, 32, false>, 64); break;
-        // fp32 at t = 256: two row tiles per wave, the residual rows re-read at the end
-        // (measured 393 -> 341 us per launch at level 3).
-        case 256: h16 ? go(k_mlp<256, 2, 32, true>, 128) : go(k_mlp<256, 2, 16, false>, 128); break;
+        // each streamed weight slice feeds 256 (t = 128) or 128 (t = 256) rows. fp32 at
+        // t = 128: 16 hidden units per slice (317 -> 314 us per launch at level 2 of 1080p).
+        case 128: h16 ? go(k_mlp<128, 2, 32, true, 8>, 256, 512) : go(k_mlp<128, 1, 16, false>, 64); break;
+        // fp32 at t = 256: 8 waves of one row tile each share every 32-unit weight slice
+        // (128 rows per workgroup; level 3 of 1080p: 337 -> 307 us per launch, against two
+        // row tiles per wave on 4 waves).
+        case 256: h16 ? go(k_mlp<256, 2, 32, true>, 128) : go(k_mlp<256, 1, 32, false, 8>, 128, 512); break;
         default: *why = "mlp: t must be 32, 64, 128 or 256"; return false;
     }
     return true;
