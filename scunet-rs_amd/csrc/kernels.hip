@@ -711,9 +711,10 @@ static bool launch_gemm3(const GemmArgs& g, GemmA a, GemmE e, hipStream_t s) {
     // the depth-to-space epilogue measured faster one tile per workgroup (k_gemm2).
     if (a == A_LN || a == A_ADD2) return false;
     // Measured on the 1080p forward: one 16-row tile per wave and a wide N block for the 1x1
-    // at 256 and 512 channels (4-6 % faster than two tiles per wave) and for the level-0
-    // down-conv (N = 128: 9 %); the other down-convs keep two tiles per wave.
-    if (a == A_ROWS && g.N >= 512 && g.N % 256 == 0) launch_gemm3_a<1, 256, 32>(g, a, e, s);
+    // at 256 and 512 channels (4-6 % faster than two tiles per wave), for the level-0
+    // down-conv (N = 128: 9 %) and for the level-2 down-conv (N = 512: 322 -> 310 us); the
+    // level-1 down-conv (N = 256) keeps two tiles per wave.
+    if ((a == A_ROWS || a == A_S2D) && g.N >= 512 && g.N % 256 == 0) launch_gemm3_a<1, 256, 32>(g, a, e, s);
     else if ((a == A_ROWS && g.N == 256) || (a == A_S2D && g.N == 128)) launch_gemm3_a<1, 128, 32>(g, a, e, s);
     else if (g.N % 64 == 0 && g.N <= 128) launch_gemm3_a<2, 64, 32>(g, a, e, s);
     else if (g.N % 128 == 0) launch_gemm3_a<2, 128, 32>(g, a, e, s);
