@@ -1251,7 +1251,9 @@ bool mlp(const MlpArgs& a, hipStream_t s, const char** why) {
         case 128: h16 ? go(k_mlp<128, 2, 32, true, 8>, 256, 512) : go(k_mlp<128, 1, 16, false>, 64); break;
         // fp32 at t = 256: 8 waves of one row tile each share every 32-unit weight slice
         // (128 rows per workgroup; level 3 of 1080p: 337 -> 307 us per launch, against two
-        // row tiles per wave on 4 waves).
+        // row tiles per wave on 4 waves). Two waves per SIMD cap it at 256 VGPRs, so it
+        // spills 54 of them to scratch, which is in that time; the spill-free 4-wave shapes
+        // measured 337 us (two row tiles per wave) and 380 us (one).
         case 256: h16 ? go(k_mlp<256, 2, 32, true>, 128) : go(k_mlp<256, 1, 32, false, 8>, 128, 512); break;
         default: *why = "mlp: t must be 32, 64, 128 or 256"; return false;
     }
