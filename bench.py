@@ -26,27 +26,66 @@ sys.path.insert(0, os.path.join(REPO, "scunet-rs_amd"))
 
 METRIC = "megapixels/sec end-to-end SCUNet-color 1920x1088; attention kernel TFLOP/s"
 PEAK_FP32_TFLOPS = 157.3      # MI355X dense fp32 matrix
+PEAK_FP16_TFLOPS = 2500.0     # MI355X dense fp16 matrix (the fp16-operand mode's products)
 PEAK_HBM_GBS = 8000.0         # MI355X HBM3E
-RIDGE = PEAK_FP32_TFLOPS * 1e12 / (PEAK_HBM_GBS * 1e9)
+# The 3x3 convolutions run as Winograd F(2x2,3x3) unless SCUNET_HIP_DIRECT3X3 is set (or in
+# the fp16 mode, which uses a direct kernel): the library counts the direct convolution's
+# 18*cin*cout FLOP per pixel for every path, the Winograd kernel executes 16 products of
+# (cout x cin) per 2x2 output tile, i.e. 8*cin*cout FLOP per pixel, on the MFMA units.
+WINOGRAD_EXECUTED = 8.0 / 18.0
 
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def roofline_of(name, launches, ms, flop, byts):
-    ai = flop / max(byts, 1.0)
-    if ai >= RIDGE:
-        ach = flop / (ms * 1e-3) / 1e12
-        return {"kernel": name, "bound": "mfma", "achieved": round(ach, 3), "peak": PEAK_FP32_TFLOPS,
-                "unit": "TFLOP/s", "frac": round(ach / PEAK_FP32_TFLOPS, 4), "traffic": None,
-                "launches": launches, "avg_launch_ms": round(ms / launches, 5),
-                "algorithmic_flop_per_launch": flop / launches, "algorithmic_bytes_per_launch": byts / launches}
+def roofline_of(name, launches, ms, flop, byts, peak_tflops=PEAK_FP32_TFLOPS, executed=1.0):
+    """Roofline figures of one kernel class. flop/byts are the library's algorithmic counts
+    summed over the launches; `executed` scales flop to what the MFMA units execute (the
+    Winograd 3x3), so `achieved` and `frac` are executed rates and frac <= 1 by
+    construction. The bound is the side of the ridge the executed work falls on."""
+    xflop = flop * executed
+    ridge = peak_tflops * 1e12 / (PEAK_HBM_GBS * 1e9)
+    base = {"kernel": name, "traffic": None, "launches": launches, "avg_launch_ms": round(ms / launches, 5),
+            "algorithmic_flop_per_launch": xflop / launches, "algorithmic_bytes_per_launch": byts / launches}
+    if xflop / max(byts, 1.0) >= ridge:
+        ach = xflop / (ms * 1e-3) / 1e12
+        return dict(base, bound="mfma", achieved=round(ach, 3), peak=peak_tflops, unit="TFLOP/s",
+                    frac=round(ach / peak_tflops, 4))
     ach = byts / (ms * 1e-3) / 1e9
-    return {"kernel": name, "bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-            "frac": round(ach / PEAK_HBM_GBS, 4), "traffic": None, "launches": launches,
-            "avg_launch_ms": round(ms / launches, 5), "algorithmic_flop_per_launch": flop / launches,
-            "algorithmic_bytes_per_launch": byts / launches}
+    return dict(base, bound="hbm", achieved=round(ach, 1), peak=PEAK_HBM_GBS, unit="GB/s",
+                frac=round(ach / PEAK_HBM_GBS, 4))
+
+
+def class_table(rows, steps, peak_tflops, winograd):
+    """Per kernel class (rows are per class and UNet level "@Lk"): roofline figures, share of
+    device time and the per-level breakdown, sorted by device time."""
+    total_ms = max(sum(r[2] for r in rows), 1e-9)
+    classes = {}
+    for name, n, ms, flop, byts in rows:
+        agg = classes.setdefault(name.split("@")[0], [0, 0.0, 0.0, 0.0])
+        agg[0] += n
+        agg[1] += ms
+        agg[2] += flop
+        agg[3] += byts
+    out = []
+    for base, (n, ms, flop, byts) in sorted(classes.items(), key=lambda kv: -kv[1][1]):
+        ex = WINOGRAD_EXECUTED if (winograd and base == "conv3x3") else 1.0
+        k = roofline_of(base, n, ms, flop, byts, peak_tflops, ex)
+        k["share"] = round(ms / total_ms, 4)
+        if ex != 1.0:
+            k["algorithm"] = ("winograd F(2x2,3x3): achieved/frac count the 8*cin*cout FLOP per pixel the MFMA "
+                              "units execute; direct_equiv_tflops counts the direct convolution's 18*cin*cout")
+            k["direct_equiv_tflops"] = round(flop / (ms * 1e-3) / 1e12, 3)
+        k["levels"] = {}
+        for name, n2, ms2, flop2, byts2 in rows:
+            if name.split("@")[0] == base and "@" in name:
+                lv = roofline_of(name, n2, ms2, flop2, byts2, peak_tflops, ex)
+                k["levels"][name.split("@")[1]] = {"achieved": lv["achieved"], "unit": lv["unit"],
+                                                   "frac": lv["frac"], "avg_launch_ms": lv["avg_launch_ms"],
+                                                   "ms_per_step": round(ms2 / steps, 4)}
+        out.append(k)
+    return out
 
 
 def measured_traffic():
@@ -60,24 +99,42 @@ def measured_traffic():
         return json.load(f).get("classes", {})
 
 
-def cpu_baseline(weights_path, x, rows):
+def cpu_baseline(weights_path, x, rows, iters):
     """The oracle (C++ restatement of the reference's src/cpu.rs, OpenMP over all host
-    threads) on a bounded sample of the benchmark's own input: the top `rows` rows of the
-    1080p image, forwarded as a whole image (same per-pixel work)."""
+    threads; it stands in for the reference's Rust CPU backend, which cannot be built here)
+    on a bounded sample of the benchmark's own input: the top `rows` rows of the 1080p
+    image, forwarded as one whole image (the same per-pixel work), 1 untimed warmup then
+    `iters` timed runs (the protocol of the reference's examples/bench.rs:151-214 for
+    configs 1-3). value = the median run's Mpx/s."""
     import numpy as np
     sys.path.insert(0, os.path.join(REPO, "oracle"))
     import oracle
     wt = oracle.Weights.load(weights_path)
     sample = np.ascontiguousarray(x[:, :rows, :])
     c, h, w = sample.shape
-    t0 = time.perf_counter()
     oracle.run(wt, sample)
-    dt = time.perf_counter() - t0
-    return {"value": round(h * w / dt / 1e6, 5), "unit": "Mpx/s", "cores": oracle.threads(), "kind": "port",
-            "sample": f"the top {h} of the benchmark image's 1080 rows ({c}x{h}x{w}, {h * w / 1e6:.2f} Mpx) forwarded "
-                      f"as one image through oracle/scunet_oracle.cpp, the C++ restatement of src/cpu.rs, "
-                      f"on {oracle.threads()} threads; {dt:.2f} s",
-            "seconds": round(dt, 3)}
+    ts = []
+    for _ in range(iters):
+        t0 = time.perf_counter()
+        oracle.run(wt, sample)
+        ts.append(time.perf_counter() - t0)
+    ts.sort()
+    med = ts[len(ts) // 2]
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except AttributeError:
+        affinity = os.cpu_count()
+    return {"value": round(h * w / med / 1e6, 5), "unit": "Mpx/s", "cores": oracle.threads(), "kind": "port",
+            "sample": f"a strip, not the full frame: the top {h} of the benchmark image's 1080 rows "
+                      f"({c}x{h}x{w}, {h * w / 1e6:.3f} Mpx) forwarded as one image through "
+                      f"oracle/scunet_oracle.cpp (the C++ restatement of src/cpu.rs) on {oracle.threads()} OpenMP "
+                      f"threads; 1 warmup + {iters} timed runs, value from the median",
+            "iterations": iters, "warmup": 1,
+            "seconds": [round(t, 3) for t in ts], "median_s": round(med, 3),
+            "spread_pct": round(100.0 * (ts[-1] - ts[0]) / med, 2),
+            "mpx_s_min_max": [round(h * w / ts[-1] / 1e6, 5), round(h * w / ts[0] / 1e6, 5)],
+            "omp_threads": oracle.threads(), "nproc": os.cpu_count(), "affinity_cpus": affinity,
+            "OMP_NUM_THREADS": os.environ.get("OMP_NUM_THREADS")}
 
 
 def attention_sweep(be, wpath, iters):
@@ -126,8 +183,9 @@ def main():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-rows", type=int, default=512,
-                    help="rows of the 1080p input the CPU baseline forwards (a multiple of 8)")
+    ap.add_argument("--cpu-rows", type=int, default=192,
+                    help="rows of the 1080p input the CPU baseline forwards (a multiple of 64)")
+    ap.add_argument("--cpu-iters", type=int, default=3, help="timed CPU-baseline runs (after 1 warmup)")
     ap.add_argument("--no-kernel-events", action="store_true",
                     help="time the steps without the per-launch event pairs")
     ap.add_argument("--no-attn-sweep", action="store_true", help="skip the config-5 attention sweep")
@@ -224,11 +282,15 @@ def main():
         for _ in range(args.warmup):
             be.run_device(xp, c, h, w, yp)
         be.synchronize()
+        be.profile(not args.no_kernel_events)
+        be.synchronize()
         t1 = time.perf_counter()
         for _ in range(args.steps):
             be.run_device(xp, c, h, w, yp)
         be.synchronize()
         dt16 = (time.perf_counter() - t1) / args.steps
+        rows16 = be.profile_rows() if not args.no_kernel_events else []
+        be.profile(False)
         y16 = be.d2h(np.empty_like(x), yp)
         be.set_precision("fp32")
         d = y16.astype(np.float64) - y.astype(np.float64)
@@ -239,56 +301,45 @@ def main():
                 "tolerance": {"max_abs": 4e-3, "psnr_db": 70.0},
                 "note": "scunet_hip_set_precision(SCUNET_HIP_FP16): fp16 MFMA operands, fp32 accumulation, "
                         "fp32 planes/LayerNorm/softmax/GELU; not the headline (the reference path is fp32)"}
+        if rows16:
+            k16 = class_table(rows16, args.steps, PEAK_FP16_TFLOPS, winograd=False)
+            flop16 = sum(r[3] for r in rows16) / args.steps
+            byts16 = sum(r[4] for r in rows16) / args.steps
+            dev16 = sum(r[2] for r in rows16) / args.steps
+            fp16["forward"] = {"tflops": round(flop16 / (dev16 * 1e-3) / 1e12, 2),
+                               "frac_of_fp16_peak": round(flop16 / (dev16 * 1e-3) / 1e12 / PEAK_FP16_TFLOPS, 4),
+                               "algorithmic_gbs": round(byts16 / (dev16 * 1e-3) / 1e9, 1),
+                               "frac_of_hbm": round(byts16 / (dev16 * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                               "device_ms_per_step": round(dev16, 3),
+                               "note": "whole forward: algorithmic FLOP (all products direct in this mode) and "
+                                       "bytes over the summed per-launch device times, against the 2.5 PFLOP/s "
+                                       "dense fp16 MFMA peak and 8 TB/s"}
+            fp16["roofline"] = k16[0]
+            fp16["kernels"] = k16
         log(f"bench: fp16 mode {dt16 * 1e3:.2f} ms/step, {fp16['value']:.2f} Mpx/s, max |diff| vs fp32 "
             f"{fp16['max_abs_vs_fp32']:.2e}, PSNR {fp16['psnr_db_vs_fp32']} dB")
+        if "forward" in fp16:
+            f = fp16["forward"]
+            log(f"bench: fp16 mode forward {f['tflops']} TFLOP/s ({100 * f['frac_of_fp16_peak']:.1f}% of the fp16 "
+                f"peak), {f['algorithmic_gbs']} GB/s ({100 * f['frac_of_hbm']:.1f}% of HBM)")
 
-    # Rows are per (kernel class, UNet level "@Lk"); aggregate per class for the roofline.
-    total_ms = max(sum(r[2] for r in rows), 1e-9)
-    classes = {}
-    for name, n, ms, flop, byts in rows:
-        base = name.split("@")[0]
-        agg = classes.setdefault(base, [0, 0.0, 0.0, 0.0])
-        agg[0] += n
-        agg[1] += ms
-        agg[2] += flop
-        agg[3] += byts
-    kernels = []
-    for base, (n, ms, flop, byts) in sorted(classes.items(), key=lambda kv: -kv[1][1]):
-        k = roofline_of(base, n, ms, flop, byts)
-        k["share"] = round(ms / total_ms, 4)
-        k["levels"] = {}
-        for name, n2, ms2, flop2, byts2 in rows:
-            if name.split("@")[0] == base and "@" in name:
-                lv = roofline_of(name, n2, ms2, flop2, byts2)
-                k["levels"][name.split("@")[1]] = {"achieved": lv["achieved"], "unit": lv["unit"],
-                                                   "frac": lv["frac"], "avg_launch_ms": lv["avg_launch_ms"],
-                                                   "ms_per_step": round(ms2 / args.steps, 4)}
-        kernels.append(k)
+    kernels = class_table(rows, args.steps, PEAK_FP32_TFLOPS, winograd=not os.environ.get("SCUNET_HIP_DIRECT3X3"))
     for k in kernels:
         log(f"  {k['kernel']:>14}: {k['launches']:5d} launches, {k['avg_launch_ms'] * 1e3:9.1f} us avg, "
             f"{k['achieved']:9.2f} {k['unit']} ({100 * k['frac']:.1f}% of {k['bound']}), share {100 * k['share']:.1f}%")
         for lvl, v in sorted(k["levels"].items()):
             log(f"  {'':>14}   {lvl}: {v['avg_launch_ms'] * 1e3:9.1f} us avg, {v['ms_per_step']:7.3f} ms/step, "
                 f"{v['achieved']:9.2f} {v['unit']} ({100 * v['frac']:.1f}%)")
-    # The conv-block 3x3 convolutions run as Winograd F(2x2,3x3) unless SCUNET_HIP_DIRECT3X3
-    # is set: `achieved` counts the direct convolution's 18*cin*cout FLOP per pixel (the
-    # algorithm of the reference), the MFMA units execute 8*cin*cout per pixel (16 products
-    # per 2x2 output tile); the transforms run on the vector ALUs and are not counted.
-    if not os.environ.get("SCUNET_HIP_DIRECT3X3"):
-        for k in kernels:
-            if k["kernel"] == "conv3x3":
-                ex = k["achieved"] * 8.0 / 18.0
-                k["algorithm"] = "winograd F(2x2,3x3); achieved/frac count direct-convolution FLOP"
-                k["executed_mfma_tflops"] = round(ex, 3)
-                k["executed_frac"] = round(ex / PEAK_FP32_TFLOPS, 4)
-                log(f"  conv3x3 (Winograd): {ex:.2f} TFLOP/s executed on MFMA "
-                    f"({100 * ex / PEAK_FP32_TFLOPS:.1f}% of peak)")
+    # Hardware-counter figures per class (profiles/counters_1080p.md): HBM bytes per launch
+    # and the MFMA-busy fraction, beside the event-timed rates above.
     traffic = measured_traffic()
     for k in kernels:
         t = traffic.get(k["kernel"])
         if t and t["launches"] * args.steps == k["launches"]:
             k["traffic"] = round(t["traffic_bytes_per_launch"])
             k["traffic_source"] = "profiles/counters_1080p.md"
+            if "mfma_busy_pct" in t:
+                k["mfma_busy_counter"] = round(t["mfma_busy_pct"] / 100.0, 4)
     dominant = kernels[0] if kernels else None
     # The forward's window attention runs inside the fused window kernels: msa_fused (LN1,
     # qkv, attention, proj, residual; levels 1-3) and tblock_fused (the same plus the MLP;
@@ -304,9 +355,11 @@ def main():
 
     cpu = None
     if not args.no_cpu_baseline:
-        log(f"bench: CPU baseline (oracle) on the top {args.cpu_rows} rows of the input ...")
-        cpu = cpu_baseline(wpath, x, args.cpu_rows)
-        log(f"bench: CPU baseline {cpu['value']} Mpx/s on {cpu['cores']} threads ({cpu['seconds']} s)")
+        log(f"bench: CPU baseline (oracle) on the top {args.cpu_rows} rows of the input, 1 warmup + "
+            f"{args.cpu_iters} timed ...")
+        cpu = cpu_baseline(wpath, x, args.cpu_rows, args.cpu_iters)
+        log(f"bench: CPU baseline {cpu['value']} Mpx/s (median) on {cpu['cores']} threads, runs {cpu['seconds']} s, "
+            f"spread {cpu['spread_pct']}%")
 
     line = {
         "metric": METRIC,

@@ -41,7 +41,31 @@ typedef void (*scunet_stage_hook)(const char* name, const float* plane, size_t n
  * tensor shape exactly as weights.rs:204-280 does, and upload (repacked) to the
  * device. Fails with a message naming the field or tensor. */
 int scunet_hip_create(const char* safetensors_path, scunet_hip** out);
-/* Message of the last failed scunet_hip_create on this thread. */
+/* The architecture of a checkpoint the caller has already loaded: the fields of the
+ * reference's `Weights` (src/weights.rs:83-97): arch.name(), in_nc, dim, head_dim, window,
+ * config ([down1, down2, down3, body, up3, up2, up1]). */
+typedef struct {
+    const char* variant;
+    size_t in_nc, dim, head_dim, window;
+    size_t config[7];
+} scunet_hip_arch_info;
+
+/* Weights::t / shape (src/weights.rs:312-320) as a callback: return the float32 data of
+ * tensor `name` (row-major) and write its shape to shape[0..*ndim) (at most 8 extents),
+ * or return NULL when there is no such tensor. The data is read during the create call
+ * only. */
+typedef const float* (*scunet_hip_tensor_lookup)(void* user, const char* name, size_t* shape,
+                                                 size_t* ndim);
+
+/* Cuda::new(&'a Weights) (src/cuda.rs:192-241) on tensors the caller has already loaded:
+ * every tensor the network uses is requested by name through `lookup`, validated
+ * exactly as scunet_hip_create validates a file (weights.rs:204-280: a missing tensor or
+ * a wrong shape fails with the same message, the file path replaced by "weights"), and
+ * uploaded. No file is read, so a checkpoint the caller mmapped is loaded once. */
+int scunet_hip_create_from_tensors(const scunet_hip_arch_info* arch, scunet_hip_tensor_lookup lookup,
+                                   void* user, scunet_hip** out);
+/* Message of the last failed scunet_hip_create or scunet_hip_create_from_tensors on this
+ * thread. */
 const char* scunet_hip_create_error(void);
 void scunet_hip_destroy(scunet_hip* h);
 /* Message of the last failed call on this handle ("" if none). */

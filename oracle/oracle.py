@@ -61,6 +61,9 @@ def lib():
         L.oracle_forward_dump.argtypes = [ctypes.POINTER(_OW), _f, _sz, _sz, _f, HOOK, ctypes.c_void_p]
         L.oracle_conv_trans_block.argtypes = [ctypes.POINTER(_OW), ctypes.c_char_p, _f, _sz, _sz, _sz,
                                               _f, _f, _f, _f, _f, _f]
+        L.oracle_forward_dump.restype = ctypes.c_int
+        L.oracle_conv_trans_block.restype = ctypes.c_int
+        L.oracle_last_error.restype = ctypes.c_char_p
         _lib = L
     return _lib
 
@@ -74,6 +77,11 @@ def _p(a):
 
 def _c32(a):
     return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def _check(rc):
+    if rc != 0:
+        raise RuntimeError(lib().oracle_last_error().decode())
 
 
 def set_threads(n):
@@ -230,8 +238,8 @@ def conv_trans_block(wt, prefix, x, shift, dump=False):
                  trans_half=np.empty((trans, h, w), np.float32),
                  msa=np.empty((h * w, trans), np.float32), res=np.empty((c, h, w), np.float32))
     args = [_p(d[k]) if d else None for k in ("expand", "conv_half", "trans_half", "msa", "res")]
-    lib().oracle_conv_trans_block(ctypes.byref(wt.ow), prefix.encode(), _p(_c32(x)), _sz(h), _sz(w),
-                                  _sz(shift), _p(out), *args)
+    _check(lib().oracle_conv_trans_block(ctypes.byref(wt.ow), prefix.encode(), _p(_c32(x)), _sz(h), _sz(w),
+                                         _sz(shift), _p(out), *args))
     return (out, d) if dump else out
 
 
@@ -247,7 +255,8 @@ def forward_dump(wt, x_padded, keep=None):
             stages[nm] = np.ctypeslib.as_array(ptr, shape=(n,)).copy()
 
     cb = HOOK(hook)
-    lib().oracle_forward_dump(ctypes.byref(wt.ow), _p(_c32(x_padded)), _sz(hp), _sz(wp), _p(out), cb, None)
+    _check(lib().oracle_forward_dump(ctypes.byref(wt.ow), _p(_c32(x_padded)), _sz(hp), _sz(wp), _p(out), cb,
+                                     None))
     return out, stages
 
 

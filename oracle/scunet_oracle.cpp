@@ -25,6 +25,7 @@
 #include <unordered_map>
 #include <vector>
 #include <cfloat>
+#include <stdexcept>
 #include <omp.h>
 
 namespace {
@@ -343,18 +344,12 @@ struct Weights {
     int config[7] = {4, 4, 4, 4, 4, 4, 4};
     const float* get(const std::string& name) const {
         auto it = t.find(name);
-        if (it == t.end()) {
-            std::fprintf(stderr, "oracle: weight `%s` missing\n", name.c_str());
-            std::abort();
-        }
+        if (it == t.end()) throw std::runtime_error("oracle: weight `" + name + "` missing");
         return it->second.first;
     }
     size_t numel(const std::string& name) const {
         auto it = t.find(name);
-        if (it == t.end()) {
-            std::fprintf(stderr, "oracle: weight `%s` missing\n", name.c_str());
-            std::abort();
-        }
+        if (it == t.end()) throw std::runtime_error("oracle: weight `" + name + "` missing");
         return it->second.second;
     }
     // weights.rs:196-200: (conv, trans) read off conv1_1.weight [c][c][1][1] and
@@ -524,15 +519,55 @@ void block_project(const float* x, std::pair<size_t, size_t> dims, size_t h, siz
 
 const char* STAGE_NAMES[7] = {"down1", "down2", "down3", "body", "up3", "up2", "up1"};
 
+thread_local std::string g_error;
+
+template <typename F>
+int guarded(F&& f) {
+    g_error.clear();
+    try {
+        f();
+        return 0;
+    } catch (const std::exception& e) {
+        g_error = e.what();
+        return 1;
+    }
+}
+
+void conv_trans_block_impl(const oracle_weights* ow, const char* prefix, const float* x, size_t h,
+                           size_t w, size_t shift, float* out, float* expand, float* conv_half,
+                           float* trans_half, float* msa, float* res);
+void forward_dump_impl(const oracle_weights* ow, const float* x, size_t hp, size_t wp,
+                       float* out_final, oracle_hook hook, void* user);
+
 }  // namespace
 
 extern "C" {
 
 // cpu.rs:976-983 (conv_trans_block) with the interior dump of cpu.rs:1000-1081.
 // Any of the dump pointers may be NULL.
+// Errors (a missing weight) return 1 with the message in oracle_last_error(): the oracle
+// shares its process with the GPU test session, which one bad input must not end.
 int oracle_conv_trans_block(const oracle_weights* ow, const char* prefix, const float* x,
                             size_t h, size_t w, size_t shift, float* out, float* expand,
                             float* conv_half, float* trans_half, float* msa, float* res) {
+    return guarded([&] { conv_trans_block_impl(ow, prefix, x, h, w, shift, out, expand, conv_half,
+                                                trans_half, msa, res); });
+}
+
+int oracle_forward_dump(const oracle_weights* ow, const float* x, size_t hp, size_t wp,
+                        float* out_final, oracle_hook hook, void* user) {
+    return guarded([&] { forward_dump_impl(ow, x, hp, wp, out_final, hook, user); });
+}
+
+const char* oracle_last_error(void) { return g_error.c_str(); }
+
+}  // extern "C"
+
+namespace {
+
+void conv_trans_block_impl(const oracle_weights* ow, const char* prefix, const float* x, size_t h,
+                           size_t w, size_t shift, float* out, float* expand, float* conv_half,
+                           float* trans_half, float* msa, float* res) {
     Weights wt = make_weights(ow);
     auto dims = wt.block_dims(prefix);
     size_t c = dims.first + dims.second, n = h * w;
@@ -541,13 +576,12 @@ int oracle_conv_trans_block(const oracle_weights* ow, const char* prefix, const 
     block_project(x, dims, h, w, size_t(wt.window), shift, wt, prefix, proj, &d);
     std::memcpy(out, x, c * n * 4);
     add_into(proj.data(), out, c * n);
-    return 0;
 }
 
 // cpu.rs:1175-1321: the walker with the 16-name stage hook. `x` is the padded
 // [in_nc][hp][wp] plane; `out` receives [in_nc][hp][wp].
-int oracle_forward_dump(const oracle_weights* ow, const float* x, size_t hp, size_t wp,
-                        float* out_final, oracle_hook hook, void* user) {
+void forward_dump_impl(const oracle_weights* ow, const float* x, size_t hp, size_t wp,
+                       float* out_final, oracle_hook hook, void* user) {
     Weights wt = make_weights(ow);
     size_t dim = size_t(wt.dim), in_nc = size_t(wt.in_nc), win = size_t(wt.window);
     size_t n = hp * wp;
@@ -622,7 +656,6 @@ int oracle_forward_dump(const oracle_weights* ow, const float* x, size_t hp, siz
     conv3x3(cur.data(), dim, in_nc, hp, wp, wt.get("m_tail.0.weight"), out.data());
     f("m_tail", out);
     std::memcpy(out_final, out.data(), out.size() * 4);
-    return 0;
 }
 
-}  // extern "C"
+}  // namespace

@@ -733,7 +733,8 @@ extern "C" {
 
 const char* scunet_hip_create_error(void) { return g_create_error.c_str(); }
 
-static int create_handle(const char* path, scunet_hip** out);
+static int create_handle(const char* path, const scunet_hip_arch_info* arch, scunet_hip_tensor_lookup lookup,
+                         void* user, scunet_hip** out);
 
 // No C++ exception leaves the C ABI: a failed host allocation while reading or repacking the
 // checkpoint is reported like any other create error.
@@ -745,17 +746,52 @@ int scunet_hip_create(const char* path, scunet_hip** out) {
     }
     *out = nullptr;
     try {
-        return create_handle(path, out);
+        return create_handle(path, nullptr, nullptr, nullptr, out);
     } catch (const std::exception& e) {
         g_create_error = std::string("scunet_hip_create: ") + e.what();
         return 1;
     }
 }
 
-static int create_handle(const char* path, scunet_hip** out) {
+int scunet_hip_create_from_tensors(const scunet_hip_arch_info* arch, scunet_hip_tensor_lookup lookup, void* user,
+                                   scunet_hip** out) {
+    g_create_error.clear();
+    if (!out) {
+        g_create_error = "null output handle";
+        return 1;
+    }
+    *out = nullptr;
+    if (!arch) {
+        g_create_error = "weights: no architecture given";
+        return 1;
+    }
+    try {
+        return create_handle(nullptr, arch, lookup, user, out);
+    } catch (const std::exception& e) {
+        g_create_error = std::string("scunet_hip_create_from_tensors: ") + e.what();
+        return 1;
+    }
+}
+
+// From a file (path) or from the caller's tensors (arch + lookup, borrowed until the upload).
+static int create_handle(const char* path, const scunet_hip_arch_info* arch, scunet_hip_tensor_lookup lookup,
+                         void* user, scunet_hip** out) {
     std::unique_ptr<scunet_hip> h(new scunet_hip());
     std::string err;
-    if (!h->wt.load(path ? path : "", &err)) {
+    if (arch) {
+        ArchInfo a;
+        a.variant = arch->variant ? arch->variant : "";
+        auto clamp = [](size_t v) { return long(std::min<size_t>(v, size_t(1) << 40)); };
+        a.in_nc = clamp(arch->in_nc);
+        a.dim = clamp(arch->dim);
+        a.head_dim = clamp(arch->head_dim);
+        a.window = clamp(arch->window);
+        for (int i = 0; i < 7; ++i) a.config[i] = clamp(arch->config[i]);
+        if (!h->wt.borrow(a, lookup, user, &err)) {
+            g_create_error = err;
+            return 1;
+        }
+    } else if (!h->wt.load(path ? path : "", &err)) {
         g_create_error = err;
         return 1;
     }
@@ -789,6 +825,7 @@ static int create_handle(const char* path, scunet_hip** out) {
         g_create_error = h->err;
         return 1;
     }
+    if (arch) h->wt.forget_data();   // the caller's buffers are not ours beyond this call
     *out = h.release();
     return 0;
 }

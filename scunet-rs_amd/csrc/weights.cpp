@@ -7,8 +7,10 @@
 #include <unistd.h>
 
 #include <cerrno>
+#include <cmath>
 #include <cstring>
 #include <memory>
+#include <set>
 #include <sstream>
 
 namespace scunet {
@@ -155,6 +157,11 @@ std::string shape_str(const std::vector<size_t>& s) {
     return o.str();
 }
 
+// A JSON number that is an integer in [0, max].
+bool whole(const JVal& v, double max) {
+    return v.kind == JVal::NUM && std::isfinite(v.num) && v.num >= 0 && v.num <= max && v.num == std::floor(v.num);
+}
+
 // weights.rs:44-60 / 76-81: the eight published variants and their in_nc.
 int variant_in_nc(const std::string& v) {
     static const char* color[] = {"color-15", "color-25", "color-50", "color-real-psnr", "color-real-gan"};
@@ -262,8 +269,22 @@ bool Weights::load(const std::string& path, std::string* err) {
         Tensor tt;
         size_t n = 1;
         for (auto& d : sh->arr) {
-            tt.shape.push_back(size_t(d.num));
-            n *= size_t(d.num);
+            // Extents are integers in [0, 2^32]; the element count may not overflow.
+            if (!whole(d, 4294967296.0)) {
+                *err = path + ": " + kv.first + ": shape entry is not an integer in [0, 2^32]";
+                return false;
+            }
+            const size_t e = size_t(d.num);
+            if (e != 0 && n > (SIZE_MAX / 4) / e) {
+                *err = path + ": " + kv.first + ": shape " + shape_str(tt.shape) + " overflows";
+                return false;
+            }
+            tt.shape.push_back(e);
+            n *= e;
+        }
+        if (!whole(off->arr[0], 9007199254740992.0) || !whole(off->arr[1], 9007199254740992.0)) {
+            *err = path + ": " + kv.first + ": data offsets are not non-negative integers";
+            return false;
         }
         size_t a = size_t(off->arr[0].num), b = size_t(off->arr[1].num);
         if (b < a || b > data_len || b - a != n * 4) {
@@ -322,7 +343,18 @@ bool Weights::load(const std::string& path, std::string* err) {
         }
         for (int i = 0; i < 7; ++i) config[i] = cfg[size_t(i)];
     }
+    // The order of weights.rs:127-160: the variant, in_nc against it, then the widths.
     variant = meta["variant"];
+    if (variant_in_nc(variant) < 0) return check_arch(path, err);
+    if (!num("in_nc", &in_nc)) return false;
+    if (in_nc != variant_in_nc(variant)) return check_arch(path, err);
+    if (!num("dim", &dim) || !num("head_dim", &head_dim) || !num("window_size", &window)) return false;
+    if (!check_arch(path, err)) return false;
+    return validate(path, err);
+}
+
+// The architecture checks of weights.rs:127-160 (variant, its in_nc, dim against head_dim).
+bool Weights::check_arch(const std::string& label, std::string* err) const {
     int want_nc = variant_in_nc(variant);
     if (want_nc < 0) {
         *err = "variant `" + variant +
@@ -330,23 +362,99 @@ bool Weights::load(const std::string& path, std::string* err) {
                "color-50, color-real-psnr, color-real-gan, gray-15, gray-25, gray-50)";
         return false;
     }
-    if (!num("in_nc", &in_nc)) return false;
     if (in_nc != want_nc) {
-        *err = path + ": variant " + variant + " implies in_nc " + std::to_string(want_nc) +
+        *err = label + ": variant " + variant + " implies in_nc " + std::to_string(want_nc) +
                ", the header says " + std::to_string(in_nc);
         return false;
     }
-    if (!num("dim", &dim) || !num("head_dim", &head_dim) || !num("window_size", &window)) return false;
     if (head_dim == 0 || dim % head_dim != 0) {
-        *err = path + ": dim " + std::to_string(dim) + " is not a multiple of head_dim " +
+        *err = label + ": dim " + std::to_string(dim) + " is not a multiple of head_dim " +
                std::to_string(head_dim);
         return false;
     }
-    return validate(path, err);
+    return true;
 }
 
-// weights.rs:204-280: every shape the walker will ask for.
-bool Weights::validate(const std::string& path, std::string* err) const {
+// Every tensor name the walker can ask for under this config: the head and tail, each
+// stage's blocks (up stages number theirs from 1), the up-convolutions (m_upN.0) and the
+// down-convolutions (m_downN.<count>).
+std::vector<std::string> Weights::expected_names() const {
+    std::vector<std::string> r = {"m_head.0.weight", "m_tail.0.weight"};
+    static const char* BLOCK[] = {
+        "conv1_1.weight", "conv1_1.bias", "conv1_2.weight", "conv1_2.bias", "conv_block.0.weight",
+        "conv_block.2.weight", "trans_block.ln1.weight", "trans_block.ln1.bias", "trans_block.ln2.weight",
+        "trans_block.ln2.bias", "trans_block.mlp.0.weight", "trans_block.mlp.0.bias",
+        "trans_block.mlp.2.weight", "trans_block.mlp.2.bias", "trans_block.msa.embedding_layer.weight",
+        "trans_block.msa.embedding_layer.bias", "trans_block.msa.linear.weight",
+        "trans_block.msa.linear.bias", "trans_block.msa.relative_position_params"};
+    for (int stage = 0; stage < 7; ++stage) {
+        const std::string m = "m_" + std::string(STAGE[stage]) + ".";
+        const int first = stage >= 4 ? 1 : 0;
+        for (int b = first; b < first + config[stage]; ++b)
+            for (const char* k : BLOCK) r.push_back(m + std::to_string(b) + "." + k);
+        if (stage >= 4) r.push_back(m + "0.weight");
+        if (stage < 3) r.push_back(m + std::to_string(config[stage]) + ".weight");
+    }
+    return r;
+}
+
+bool Weights::borrow(const ArchInfo& a, TensorLookup lookup, void* user, std::string* err) {
+    const std::string label = "weights";
+    if (!lookup) {
+        *err = label + ": no tensor lookup given";
+        return false;
+    }
+    auto fits = [](long v) { return v >= 0 && v <= 1 << 20; };
+    if (!fits(a.in_nc) || !fits(a.dim) || !fits(a.head_dim) || !fits(a.window)) {
+        *err = label + ": in_nc, dim, head_dim and window must be integers in [0, 2^20]";
+        return false;
+    }
+    for (int i = 0; i < 7; ++i)
+        if (a.config[i] < 1 || a.config[i] > 1024) {
+            *err = label + ": config[" + std::to_string(i) + "] = " + std::to_string(a.config[i]) +
+                   ": every stage needs between 1 and 1024 blocks";
+            return false;
+        }
+    variant = a.variant;
+    in_nc = int(a.in_nc);
+    dim = int(a.dim);
+    head_dim = int(a.head_dim);
+    window = int(a.window);
+    for (int i = 0; i < 7; ++i) config[i] = int(a.config[i]);
+    if (!check_arch(label, err)) return false;
+    t_.clear();
+    for (const std::string& n : expected_names()) {
+        size_t shape[MAX_NDIM] = {}, ndim = 0;
+        const float* p = lookup(user, n.c_str(), shape, &ndim);
+        if (!p) continue;   // validate() names the first missing tensor
+        if (ndim > MAX_NDIM) {
+            *err = label + ": " + n + ": more than " + std::to_string(MAX_NDIM) + " dimensions";
+            return false;
+        }
+        Tensor tt;
+        size_t count = 1;
+        for (size_t i = 0; i < ndim; ++i) {
+            if (shape[i] > (size_t(1) << 32) || (shape[i] != 0 && count > (SIZE_MAX / 4) / shape[i])) {
+                *err = label + ": " + n + ": shape overflows";
+                return false;
+            }
+            tt.shape.push_back(shape[i]);
+            count *= shape[i];
+        }
+        tt.data = p;
+        tt.numel = count;
+        t_[n] = tt;
+    }
+    return validate(label, err);
+}
+
+void Weights::forget_data() {
+    for (auto& kv : t_) kv.second.data = nullptr;
+}
+
+// weights.rs:204-280: every shape the walker will ask for. Tensors outside that list are
+// dropped, so nothing unchecked is uploaded.
+bool Weights::validate(const std::string& path, std::string* err) {
     std::vector<std::pair<std::string, std::vector<size_t>>> want;
     size_t d = size_t(dim), nc = size_t(in_nc), ws = size_t(window);
     want.push_back({"m_head.0.weight", {d, nc, 3, 3}});
@@ -408,6 +516,7 @@ bool Weights::validate(const std::string& path, std::string* err) const {
                             {size_t(ch.second), size_t(ch.first), 2, 2}});
         }
     }
+    std::set<std::string> checked;
     for (auto& w : want) {
         if (!present(w.first)) return false;
         const auto& got = t(w.first).shape;
@@ -417,7 +526,9 @@ bool Weights::validate(const std::string& path, std::string* err) const {
                    "-channel architecture in the header implies " + shape_str(w.second);
             return false;
         }
+        checked.insert(w.first);
     }
+    for (auto it = t_.begin(); it != t_.end();) it = checked.count(it->first) ? std::next(it) : t_.erase(it);
     return true;
 }
 

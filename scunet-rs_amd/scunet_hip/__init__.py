@@ -22,7 +22,7 @@ LIB_PATH = os.path.join(_HERE, "..", "lib", "libscunet_hip.so")
 
 # The symbols include/scunet_hip.h declares.
 EXPORTS = [
-    "scunet_hip_create", "scunet_hip_create_error", "scunet_hip_destroy", "scunet_hip_last_error",
+    "scunet_hip_create", "scunet_hip_create_from_tensors", "scunet_hip_create_error", "scunet_hip_destroy", "scunet_hip_last_error",
     "scunet_hip_name", "scunet_hip_arch", "scunet_hip_variant", "scunet_hip_set_precision", "scunet_hip_precision",
     "scunet_hip_forward", "scunet_hip_forward_device",
     "scunet_hip_forward_dump", "scunet_hip_run", "scunet_hip_run_device", "scunet_hip_run_batch",
@@ -39,6 +39,15 @@ _f = ctypes.POINTER(ctypes.c_float)
 _sz = ctypes.c_size_t
 _vp = ctypes.c_void_p
 HOOK = ctypes.CFUNCTYPE(None, ctypes.c_char_p, _f, ctypes.c_size_t, ctypes.c_void_p)
+# scunet_hip_tensor_lookup: (user, name, shape[8], ndim) -> data pointer or NULL.
+LOOKUP = ctypes.CFUNCTYPE(ctypes.c_void_p, ctypes.c_void_p, ctypes.c_char_p, ctypes.POINTER(_sz),
+                          ctypes.POINTER(_sz))
+
+
+class ArchInfo(ctypes.Structure):
+    """scunet_hip_arch_info: the fields of the reference's Weights (weights.rs:83-97)."""
+    _fields_ = [("variant", ctypes.c_char_p), ("in_nc", _sz), ("dim", _sz), ("head_dim", _sz),
+                ("window", _sz), ("config", _sz * 7)]
 
 
 class BackendError(RuntimeError):
@@ -59,6 +68,7 @@ def load_library(path=None):
     L = ctypes.CDLL(p)
     L.scunet_hip_create.argtypes = [ctypes.c_char_p, ctypes.POINTER(_vp)]
     L.scunet_hip_create_error.restype = ctypes.c_char_p
+    L.scunet_hip_create_from_tensors.argtypes = [ctypes.POINTER(ArchInfo), LOOKUP, _vp, ctypes.POINTER(_vp)]
     L.scunet_hip_destroy.argtypes = [_vp]
     L.scunet_hip_last_error.argtypes = [_vp]
     L.scunet_hip_last_error.restype = ctypes.c_char_p
@@ -167,10 +177,17 @@ class Hip:
     """``impl Backend`` for the MI355X library. Construction mirrors ``Cuda::new``
     (src/cuda.rs:192-241) over ``Weights::load`` (src/weights.rs:101-185)."""
 
-    def __init__(self, weights_path, lib_path=None):
+    def __init__(self, weights_path=None, lib_path=None, *, tensors=None, arch=None):
+        """From a safetensors file (``weights_path``), or, like ``Cuda::new(&Weights)``, from
+        tensors the caller already holds: ``tensors`` maps names to float32 arrays and
+        ``arch`` gives variant, in_nc, dim, head_dim, window and config
+        (scunet_hip_create_from_tensors)."""
         self._lib = load_library(lib_path)
         h = _vp()
-        rc = self._lib.scunet_hip_create(os.fsencode(weights_path), ctypes.byref(h))
+        if tensors is not None:
+            rc = self._create_from_tensors(tensors, arch, h)
+        else:
+            rc = self._lib.scunet_hip_create(os.fsencode(weights_path), ctypes.byref(h))
         if rc != 0:
             raise BackendError(self._lib.scunet_hip_create_error().decode())
         self._h = h
@@ -180,6 +197,26 @@ class Hip:
         self.in_nc, self.dim, self.head_dim, self.window = (v.value for v in a)
         self.config = list(cfg)
         self.variant = self._lib.scunet_hip_variant(h).decode()
+
+    def _create_from_tensors(self, tensors, arch, h):
+        held = {k: np.ascontiguousarray(v, dtype=np.float32) for k, v in tensors.items()}
+
+        def lookup(_user, name, shape, ndim):
+            a = held.get(name.decode())
+            if a is None:
+                return None
+            if a.ndim > 8:
+                ndim[0] = a.ndim
+                return a.ctypes.data
+            for i, e in enumerate(a.shape):
+                shape[i] = e
+            ndim[0] = a.ndim
+            return a.ctypes.data
+
+        cb = LOOKUP(lookup)
+        info = ArchInfo(str(arch["variant"]).encode(), int(arch["in_nc"]), int(arch["dim"]),
+                        int(arch["head_dim"]), int(arch["window"]), (_sz * 7)(*[int(v) for v in arch["config"]]))
+        return self._lib.scunet_hip_create_from_tensors(ctypes.byref(info), cb, None, ctypes.byref(h))
 
     # -- lifetime --
     def close(self):

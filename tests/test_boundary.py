@@ -120,3 +120,85 @@ def test_product_never_reaches_the_oracle():
             if f.endswith((".py", ".hip", ".cpp", ".h", "Makefile")):
                 text = open(os.path.join(root, f), errors="replace").read()
                 assert "oracle" not in text.lower(), os.path.join(root, f)
+
+
+def _arch_of(meta):
+    return {"variant": meta["variant"], "in_nc": int(meta["in_nc"]), "dim": int(meta["dim"]),
+            "head_dim": int(meta["head_dim"]), "window": int(meta["window_size"]),
+            "config": [int(v) for v in meta["config"].split(",")]}
+
+
+@pytest.mark.parametrize("mutate", [
+    lambda t, m: t.__setitem__("m_body.2.conv_block.0.weight", np.zeros((256, 256, 3, 1), np.float32)),
+    lambda t, m: t.pop("m_up2.3.trans_block.ln2.bias"),
+    lambda t, m: t.pop("m_down3.4.weight"),
+    lambda t, m: t.__setitem__("m_up1.0.weight", np.zeros((128, 64, 2), np.float32)),
+    lambda t, m: m.__setitem__("variant", "color-99"),
+    lambda t, m: m.__setitem__("in_nc", "1"),
+    lambda t, m: m.__setitem__("head_dim", "48"),
+])
+def test_create_from_tensors_fails_like_create(tmp_path, mutate):
+    """scunet_hip_create_from_tensors (Cuda::new over an already-loaded Weights, cuda.rs:192)
+    runs the checks of weights.rs:127-280 that scunet_hip_create runs on a file, with the
+    same message (the file path replaced by "weights"), before any device is touched."""
+    from scunet_hip import Hip, BackendError, LIB_PATH
+    from scunet_hip.safetensors_io import read_safetensors, write_safetensors
+    from scunet_hip import synth
+    if not os.path.exists(LIB_PATH):
+        pytest.skip("library not built")
+    t, meta = read_safetensors(synth.weights_file(seed=0))
+    t = {k: np.array(v) for k, v in t.items()}
+    meta = dict(meta)
+    mutate(t, meta)
+    p = str(tmp_path / "bad.safetensors")
+    write_safetensors(p, t, meta)
+    with pytest.raises(BackendError) as from_file:
+        Hip(p)
+    with pytest.raises(BackendError) as from_tensors:
+        Hip(tensors=t, arch=_arch_of(meta))
+    assert str(from_tensors.value) == str(from_file.value).replace(p, "weights")
+
+
+def test_create_from_tensors_checks_its_arguments():
+    from scunet_hip import Hip, BackendError, LIB_PATH
+    from scunet_hip.safetensors_io import read_safetensors
+    from scunet_hip import synth
+    if not os.path.exists(LIB_PATH):
+        pytest.skip("library not built")
+    t, meta = read_safetensors(synth.weights_file(seed=0))
+    arch = _arch_of(meta)
+    with pytest.raises(BackendError, match=r"config\[3\] = 0"):
+        Hip(tensors=t, arch=dict(arch, config=[4, 4, 4, 0, 4, 4, 4]))
+    # Extra tensors are not asked for and do not matter; a missing one is named.
+    with pytest.raises(BackendError, match="weights: m_head.0.weight: no such tensor"):
+        Hip(tensors={k: v for k, v in t.items() if k != "m_head.0.weight"}, arch=arch)
+
+
+def _raw_safetensors(path, header):
+    import json
+    import struct
+    hb = json.dumps(header).encode()
+    with open(path, "wb") as f:
+        f.write(struct.pack("<Q", len(hb)))
+        f.write(hb)
+        f.write(b"\0" * 64)
+
+
+@pytest.mark.parametrize("shape,offsets,msg", [
+    ([-1, 4], [0, 16], "not an integer in [0, 2^32]"),
+    ([2.5, 4], [0, 40], "not an integer in [0, 2^32]"),
+    ([2 ** 33], [0, 16], "not an integer in [0, 2^32]"),
+    ([2 ** 32, 2 ** 32, 2 ** 32], [0, 16], "overflows"),
+    ([4], [-16, 0], "data offsets are not non-negative integers"),
+    ([4], [0, 8], "data offsets disagree with its shape"),
+])
+def test_header_shapes_and_offsets_are_checked(tmp_path, shape, offsets, msg):
+    """A crafted header cannot make the loader size a copy from a wrapped element count."""
+    from scunet_hip import Hip, BackendError, LIB_PATH
+    if not os.path.exists(LIB_PATH):
+        pytest.skip("library not built")
+    p = str(tmp_path / "crafted.safetensors")
+    _raw_safetensors(p, {"x": {"dtype": "F32", "shape": shape, "data_offsets": offsets}})
+    with pytest.raises(BackendError) as e:
+        Hip(p)
+    assert msg in str(e.value)

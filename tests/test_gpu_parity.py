@@ -63,6 +63,27 @@ def test_backend_identity(be):
     assert w >= 4 * 18_000_000          # the whole checkpoint is resident after create
 
 
+def test_create_from_tensors_equals_create_from_file(be, weights_path):
+    """scunet_hip_create_from_tensors (Cuda::new over the caller's loaded Weights,
+    cuda.rs:192-241): the same network, bit for bit, as the handle that read the file, and
+    the caller's buffers are not needed after the call."""
+    from scunet_hip import Hip, run
+    from scunet_hip.safetensors_io import read_safetensors
+    from scunet_hip import synth
+    t, meta = read_safetensors(weights_path)
+    t = {k: np.array(v) for k, v in t.items()}
+    arch = {"variant": meta["variant"], "in_nc": 3, "dim": 64, "head_dim": 32, "window": 8,
+            "config": [4] * 7}
+    x = synth.config_input(1)
+    with Hip(tensors=t, arch=arch) as h2:
+        for v in t.values():
+            v[...] = np.nan            # the library copied what it needed during create
+        assert (h2.in_nc, h2.dim, h2.head_dim, h2.window, h2.config) == (3, 64, 32, 8, [4] * 7)
+        assert h2.variant == meta["variant"]
+        assert be.footprint()[0] == h2.footprint()[0]
+        assert np.array_equal(run(be, x), run(h2, x))
+
+
 def test_forward_rejects_wrong_shapes(be):
     from scunet_hip import BackendError, Plan
     with pytest.raises(BackendError):

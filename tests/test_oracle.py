@@ -259,3 +259,15 @@ def test_pad_crop_and_plan_geometry():
     p = O.pad_replicate(x, 8, 9)
     assert np.array_equal(p, np.pad(x, ((0, 0), (0, 3), (0, 2)), mode="edge"))
     assert np.array_equal(O.crop(p, 5, 7), x)
+
+
+def test_missing_weight_raises_instead_of_aborting(owt):
+    # The oracle shares its process with the GPU test session: a missing tensor must surface
+    # as a Python exception naming it, not end the process.
+    t = {k: v for k, v in owt.t.items() if k != "m_down1.0.conv1_2.bias"}
+    wt = O.Weights(t, owt.meta)
+    x = np.zeros((64, 64, 64), np.float32)
+    with pytest.raises(RuntimeError, match="m_down1.0.conv1_2.bias"):
+        O.conv_trans_block(wt, "m_down1.0", x, 0)
+    with pytest.raises(RuntimeError, match="m_down1.0.conv1_2.bias"):
+        O.forward(wt, np.zeros((3, 64, 64), np.float32))
