@@ -112,6 +112,21 @@ int scunet_hip_forward_dump(scunet_hip* h, const float* x, size_t c, size_t hp, 
 int scunet_hip_run(scunet_hip* h, const float* x, size_t c, size_t hh, size_t ww, float* y);
 int scunet_hip_run_device(scunet_hip* h, const float* x, size_t c, size_t hh, size_t ww, float* y);
 
+/* scunet_hip_run_device for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc). No counterpart in
+ * the reference. Same arguments and result as scunet_hip_run_device (device pointers,
+ * stream-ordered on the handle's stream), but the forward's scratch is a static device
+ * array of 256 MiB per GPU, which the library holds from the first handle created on that
+ * GPU until the process ends: no hipMalloc, hipFree or other allocation happens in the
+ * call. Limit: the padded image needs 1600 bytes of scratch per pixel (plus 256-byte
+ * alignment per role), so padded planes up to about 167 000 pixels fit (384x384, 512x320);
+ * a larger image fails with an error naming both sizes. Every call on one GPU shares
+ * that GPU's array: calls that overlap in time on one GPU (two handles, two threads or
+ * streams) race and corrupt each other's results; serialise them. Profiling events are
+ * not recorded during the call. */
+int scunet_hip_run_device_noalloc(scunet_hip* h, const float* x, size_t c, size_t hh, size_t ww,
+                                  float* y);
+
 /* n images of one size, [n][c][hh][ww] in and out, host buffers (backend::run,
  * backend.rs:63-105, over a batch): one upload, one forward over the n padded images stacked
  * along y as one plane (every kernel keeps each image's edges as plane edges, so each

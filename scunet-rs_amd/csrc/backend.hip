@@ -18,6 +18,7 @@
 #include <cstring>
 #include <map>
 #include <memory>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -27,9 +28,39 @@
 
 using namespace scunet;
 
+// The forward's scratch for callers that cannot allocate device memory
+// (scunet_hip_run_device_noalloc): every arena role of one forward, carved out of this
+// array. Each device the library runs on holds its own copy until the process ends. In
+// host code `scratch` is only a stand-in for the symbol: its device address comes from
+// hipGetSymbolAddress, resolved once per device when a handle is created on it.
+constexpr size_t NOALLOC_SCRATCH_BYTES = size_t(256) << 20;
+static __device__ __align__(256) float scratch[NOALLOC_SCRATCH_BYTES / sizeof(float)];
+
 namespace {
 
 thread_local std::string g_create_error;
+
+// Per-device address of `scratch` (null until resolved) and the error of a failed resolve.
+constexpr int MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+float* g_scratch_ptr[MAX_DEVICES] = {};
+std::string g_scratch_err[MAX_DEVICES];
+
+// With `device` current: look up the device address of `scratch` once for that device.
+void resolve_scratch(int device) {
+    if (device < 0 || device >= MAX_DEVICES) return;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_ptr[device]) return;
+    void* p = nullptr;
+    hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+        hipGetLastError();
+        g_scratch_err[device] = std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e);
+        return;
+    }
+    g_scratch_ptr[device] = static_cast<float*>(p);
+    g_scratch_err[device].clear();
+}
 
 const char* STAGE[7] = {"down1", "down2", "down3", "body", "up3", "up2", "up1"};
 
@@ -57,6 +88,10 @@ struct scunet_hip {
 
     // Arena: role -> (pointer, bytes), grown on demand, kept across calls.
     std::map<std::string, std::pair<float*, size_t>> arena;
+    // During scunet_hip_run_device_noalloc: role -> (pointer into the static scratch, bytes);
+    // buf() then serves only these and never allocates.
+    std::map<std::string, std::pair<float*, size_t>> fixed;
+    bool fixed_active = false;
 
     bool prof = false;
     bool unfused_msa = false;            // route every level through the 3-launch attention half
@@ -108,6 +143,15 @@ bool launched(scunet_hip* h, const char* what) {
 
 float* buf(scunet_hip* h, const std::string& role, size_t floats) {
     size_t bytes = std::max<size_t>(floats, 1) * sizeof(float);
+    if (h->fixed_active) {
+        auto it = h->fixed.find(role);
+        if (it == h->fixed.end() || it->second.second < bytes) {
+            fail(h, "no-alloc forward: scratch role `" + role + "` (" + std::to_string(bytes) +
+                        " bytes) is not in the planned layout");
+            return nullptr;
+        }
+        return it->second.first;
+    }
     auto& slot = h->arena[role];
     if (slot.second >= bytes) return slot.first;
     if (slot.first) {
@@ -806,6 +850,7 @@ static int create_handle(const char* path, const scunet_hip_arch_info* arch, scu
         return 1;
     }
     hipGetDevice(&h->device);
+    resolve_scratch(h->device);
     if (hipStreamCreateWithFlags(&h->stream, hipStreamNonBlocking) != hipSuccess) {
         g_create_error = "hipStreamCreate failed";
         return 1;
@@ -901,6 +946,53 @@ int scunet_hip_run_device(scunet_hip* h, const float* x, size_t c, size_t hh, si
             return fail(h, "expected " + std::to_string(h->wt.in_nc) + " channels, got " + std::to_string(c));
         size_t hp = pad64(hh), wp = pad64(ww);
         if (!preflight(h, hp, wp, 0, false)) return false;
+        return walk(h, x, int(hh), int(ww), int(hp), int(wp), y, int(hh), int(ww), nullptr, nullptr);
+    });
+}
+
+// scunet_hip_run_device with the arena in the static `scratch` array: no device memory is
+// allocated or freed. The roles of arena_plan() are laid out back to back (256-byte
+// aligned); nothing in them needs clearing, since every role is written before it is read
+// within the forward. Profiling events are not recorded during the call.
+int scunet_hip_run_device_noalloc(scunet_hip* h, const float* x, size_t c, size_t hh, size_t ww, float* y) {
+    return guard(h, [&] {
+        if (!check_min_size(h, hh, ww)) return false;
+        if (c != size_t(h->wt.in_nc))
+            return fail(h, "expected " + std::to_string(h->wt.in_nc) + " channels, got " + std::to_string(c));
+        const size_t hp = pad64(hh), wp = pad64(ww);
+        float* base = nullptr;
+        {
+            std::lock_guard<std::mutex> lock(g_scratch_mu);
+            if (h->device >= 0 && h->device < MAX_DEVICES) {
+                base = g_scratch_ptr[h->device];
+                if (!base) return fail(h, "no-alloc forward: " + g_scratch_err[h->device]);
+            }
+        }
+        if (!base) return fail(h, "no-alloc forward: device " + std::to_string(h->device) + " has no scratch");
+        std::map<std::string, std::pair<float*, size_t>> roles;
+        size_t at = 0;
+        for (auto& r : arena_plan(h, hp, wp, 0, false)) {
+            const size_t bytes = std::max<size_t>(r.second, 1) * sizeof(float);
+            roles[r.first] = {base + at / sizeof(float), bytes};
+            at += (bytes + 255) / 256 * 256;
+        }
+        if (at > NOALLOC_SCRATCH_BYTES)
+            return fail(h, "no-alloc forward: a " + std::to_string(hh) + "x" + std::to_string(ww) + " image (padded " +
+                               std::to_string(hp) + "x" + std::to_string(wp) + ") needs " + std::to_string(at) +
+                               " bytes of scratch; the static scratch holds " +
+                               std::to_string(NOALLOC_SCRATCH_BYTES) + " (use scunet_hip_run_device)");
+        struct Restore {
+            scunet_hip* h;
+            bool prof;
+            ~Restore() {
+                h->fixed_active = false;
+                h->fixed.clear();
+                h->prof = prof;
+            }
+        } restore{h, h->prof};
+        h->fixed = std::move(roles);
+        h->fixed_active = true;
+        h->prof = false;
         return walk(h, x, int(hh), int(ww), int(hp), int(wp), y, int(hh), int(ww), nullptr, nullptr);
     });
 }

@@ -25,7 +25,8 @@ EXPORTS = [
     "scunet_hip_create", "scunet_hip_create_from_tensors", "scunet_hip_create_error", "scunet_hip_destroy", "scunet_hip_last_error",
     "scunet_hip_name", "scunet_hip_arch", "scunet_hip_variant", "scunet_hip_set_precision", "scunet_hip_precision",
     "scunet_hip_forward", "scunet_hip_forward_device",
-    "scunet_hip_forward_dump", "scunet_hip_run", "scunet_hip_run_device", "scunet_hip_run_batch",
+    "scunet_hip_forward_dump", "scunet_hip_run", "scunet_hip_run_device", "scunet_hip_run_device_noalloc",
+    "scunet_hip_run_batch",
     "scunet_hip_device_need", "scunet_hip_footprint",
     "scunet_hip_release_scratch", "scunet_hip_synchronize", "scunet_hip_stream", "scunet_hip_profile",
     "scunet_hip_profile_report", "scunet_hip_malloc", "scunet_hip_free", "scunet_hip_h2d", "scunet_hip_d2h",
@@ -85,6 +86,7 @@ def load_library(path=None):
     L.scunet_hip_forward_dump.argtypes = [_vp, _f, _sz, _sz, _sz, _f, HOOK, _vp]
     L.scunet_hip_run.argtypes = [_vp, _f, _sz, _sz, _sz, _f]
     L.scunet_hip_run_device.argtypes = [_vp, _vp, _sz, _sz, _sz, _vp]
+    L.scunet_hip_run_device_noalloc.argtypes = [_vp, _vp, _sz, _sz, _sz, _vp]
     L.scunet_hip_run_batch.argtypes = [_vp, _f, _sz, _sz, _sz, _sz, _f]
     L.scunet_hip_device_need.argtypes = [_vp, _sz, _sz, _sz, ctypes.c_int, ctypes.POINTER(_sz), ctypes.POINTER(_sz)]
     L.scunet_hip_footprint.argtypes = [_vp, ctypes.POINTER(_sz), ctypes.POINTER(_sz)]
@@ -337,6 +339,11 @@ class Hip:
 
     def run_device(self, xptr, c, h, w, yptr):
         self._check(self._lib.scunet_hip_run_device(self._h, _vp(xptr), c, h, w, _vp(yptr)))
+
+    def run_device_noalloc(self, xptr, c, h, w, yptr):
+        """run_device with the forward's scratch in the library's static device array
+        (scunet_hip_run_device_noalloc): no device allocation in the call."""
+        self._check(self._lib.scunet_hip_run_device_noalloc(self._h, _vp(xptr), c, h, w, _vp(yptr)))
 
     def synchronize(self):
         self._check(self._lib.scunet_hip_synchronize(self._h))
