@@ -98,6 +98,8 @@ struct scunet_hip {
     bool direct3x3 = false;              // the direct implicit-GEMM 3x3 instead of Winograd
     bool wino16 = false;                 // Winograd with 16 output channels per unit only
     bool wino_pair = false;              // 16-channel Winograd always in 8 x 16 pair units
+    bool wino2 = false;                  // the 32-bit-offset Winograd forms wherever the plane allows
+    bool wino3_all = false;              // k_wino3 at every level (32-channel units below 64 channels)
     bool gemm2 = false;                  // one tile per workgroup GEMM (no persistent walker)
     bool gemm1x1 = false;                // the tiled GEMM for every 1x1 (no resident weights, no chaining)
     bool separate_mlp = false;           // the MLP as its own kernel also at t = 32
@@ -254,6 +256,11 @@ bool upload_weights(scunet_hip* h) {
                     for (size_t tap = 0; tap < 9; ++tap) v[(tap * co + o) * ci + i] = t.data[(o * ci + i) * 9 + tap];
             std::vector<float> u(16 * co * ci);
             winograd_filter(t.data, int(co), int(ci), u.data());
+            if (ci % 8 == 0) {
+                std::vector<float> u8(16 * co * ci);
+                winograd_filter_slices(u.data(), int(co), int(ci), u8.data());
+                host.push_back({"@wino8:" + n, std::move(u8)});
+            }
             host.push_back({"@wino:" + n, std::move(u)});
         } else if (is_down(n)) {
             size_t co = t.shape[0], ci = t.shape[1];
@@ -289,7 +296,7 @@ bool upload_weights(scunet_hip* h) {
             return false;
         if (e.first.rfind("@tab:", 0) == 0) h->tab[e.first.substr(5)] = reinterpret_cast<float*>(at);
         else if (e.first.rfind("@atab:", 0) == 0) h->atab[e.first.substr(6)] = reinterpret_cast<float*>(at);
-        else h->w[e.first] = reinterpret_cast<float*>(at);   // "@wino:<name>" are Winograd filters
+        else h->w[e.first] = reinterpret_cast<float*>(at);   // "@wino:" / "@wino8:" are Winograd filters
         at += (e.second.size() * 4 + 255) / 256 * 256;
     }
     return true;
@@ -376,8 +383,10 @@ bool run_conv3(scunet_hip* h, const std::string& name, Conv3Args c, bool relu) {
         if (!conv3x3_h16(c, relu, h->stream, &why)) return fail(h, why);
     } else if (!h->direct3x3 && u && c.cin % 16 == 0 && c.cout % 16 == 0 && c.H % 2 == 0 && c.W % 2 == 0) {
         c.w = u;
+        c.w8 = W(h, "@wino8:" + name + ".weight");
         c.cblock = h->wino16 ? 16 : 0;
         c.pair = h->wino_pair ? 1 : 0;
+        c.wino3 = h->wino2 ? 0 : h->wino3_all ? 2 : 1;
         if (!conv3x3_winograd(c, relu, h->stream, &why)) return fail(h, why);
     } else {
         c.w = W(h, name + ".weight");
@@ -863,6 +872,10 @@ static int create_handle(const char* path, const scunet_hip_arch_info* arch, scu
     h->wino16 = std::getenv("SCUNET_HIP_WINO16") != nullptr;
     // A/B switch: 16-channel Winograd units always as pairs of 8 x 16 half-tiles.
     h->wino_pair = std::getenv("SCUNET_HIP_WINO_PAIR") != nullptr;
+    // A/B switch: k_wino2 / k_wino at every level whose plane fits 32-bit offsets (no k_wino3).
+    h->wino2 = std::getenv("SCUNET_HIP_WINO2") != nullptr;
+    // A/B switch: k_wino3 at every level, including 32-channel units at level 0.
+    h->wino3_all = std::getenv("SCUNET_HIP_WINO3") != nullptr;
     h->gemm2 = std::getenv("SCUNET_HIP_GEMM2") != nullptr;
     h->gemm1x1 = std::getenv("SCUNET_HIP_GEMM1X1") != nullptr;
     h->separate_mlp = std::getenv("SCUNET_HIP_SEPARATE_MLP") != nullptr;

@@ -124,6 +124,9 @@ struct Conv3Args {
     int cblock = 0;                // Winograd: output channels per unit (0 = 32 below 256 input channels, else 16; 16)
     int pair = 0;                  // Winograd, 16-channel units: 0 = 8 x 16 pair units when they take fewer rounds, 1 = always
     const half_t* w16 = nullptr;   // fp16 mode: [9][cout][cin] k-permuted (conv3x3_h16)
+    const float* w8 = nullptr;     // Winograd: U as [cin / 8][16][cout][8] (k_wino3; null: not used)
+    int wino3 = 1;                 // Winograd: 1 k_wino3 at >= 64 channels; 0 the 32-bit-offset forms
+                                   // where the plane allows; 2 k_wino3 everywhere
 };
 // relu=true: out = relu(conv); relu=false: out += conv (the conv half's residual).
 bool conv3x3(const Conv3Args& a, bool relu, hipStream_t s, const char** why);
@@ -135,6 +138,8 @@ bool conv3x3_winograd(const Conv3Args& a, bool relu, hipStream_t s, const char**
 bool conv3x3_h16(const Conv3Args& a, bool relu, hipStream_t s, const char** why);
 // Host-side filter transform: g [cout][cin][3][3] -> U [16][cout][cin] (in double).
 void winograd_filter(const float* g, int cout, int cin, float* u);
+// U [16][cout][cin] -> [cin / 8][16][cout][8] (cin a multiple of 8), k_wino3's layout.
+void winograd_filter_slices(const float* u, int cout, int cin, float* u8);
 
 struct AttnArgs {
     const float* qkv = nullptr;    // rows of [q | k | v], each C wide

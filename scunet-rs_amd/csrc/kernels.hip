@@ -1900,6 +1900,269 @@ __global__ __launch_bounds__(512) void k_wino2(Conv3Args a, long tiles, long uni
     }
 }
 
+// ---------------------------------------------------------------------------
+// Winograd F(2x2, 3x3), the small-footprint form: a unit is 8 x 16 output pixels (4 x 8
+// tiles) x CB output channels (CB = 32 or 64), 4 waves, and the input channels go in
+// slices of 8 whose halo (10 x 18 pixels) and filter part (16 xi x CB x 8) are
+// double-buffered in LDS: 46 KB at CB = 32 (three workgroups per CU), 78 KB at CB = 64
+// (two per CU). On gfx950 the fp32 matrix instructions and the VALU do not overlap (each
+// VALU instruction delays the products by about as long as it takes), so the design
+// keeps VALU per product low and lets the independent workgroups of a CU cover each
+// other's barriers and epilogues:
+//   - wave pair p owns tile rows 2p, 2p + 1 (16 tiles, lane li = tile) and each wave of the
+//     pair owns two of the four rows of the transformed 4x4 positions for all CB output
+//     channels: the input transform costs 1 VALU instruction per product at CB = 32 and
+//     0.5 at CB = 64;
+//   - halo and filter slices come in through buffer loads whose per-thread byte offsets
+//     are fixed (the filter slice) or fixed per unit (the halo; positions outside the image
+//     get an offset past the buffer range, which loads zeros), on 64-bit unit bases, so the
+//     plane may exceed 2^32 elements;
+//   - the filters are read in the layout [cin / 8][16 xi][cout][8] (one contiguous block per
+//     slice), their 8-byte LDS slots XOR-swizzled by (row >> 2) & 3 so that the operand
+//     reads are at the two-pass minimum;
+//   - the output transform is linear in the rows: each wave forms the partial 2x2 outputs
+//     of its rows, the pair exchanges half of the channel blocks through LDS, and each
+//     wave finishes (ReLU or residual) and stores its half.
+// The next step's slice (across unit boundaries too) is loaded while the current one is
+// multiplied; one barrier per slice.
+// ---------------------------------------------------------------------------
+typedef float f2 __attribute__((ext_vector_type(2)));
+DEVI f2 ld2(const float* p) { return *reinterpret_cast<const f2*>(p); }
+DEVI void st2(float* p, f2 v) { *reinterpret_cast<f2*>(p) = v; }
+// Raw buffer loads: a descriptor (base, 2 GB range, the gfx9 word 3) in scalar registers and
+// a 32-bit per-lane byte offset; offsets at or past the range load zeros.
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+DEVI rsrc_t rsrc(const float* base) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), (short)0, 0x7fffffff, 0x00020000);
+}
+DEVI f4 bld4(rsrc_t r, int voff, int soff) {
+    return __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+}
+
+template <int CB, bool RELU, bool BATCH>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(CB == 32 ? 3 : 2, CB == 32 ? 3 : 2))) void k_wino3(Conv3Args a, int tx, int nb, int spatial, int units) {
+    // a.w8: the filters as [cin / 8][16][cout][8].
+    constexpr int BK = 8, PP = 10, HC = 18, HR = 10, NCB = CB / 16, NU = CB / 8;
+    constexpr int HSZ = HR * HC * PP;      // 1800 floats
+    constexpr int USZ = 16 * CB * BK;      // 4096 floats
+    constexpr int BSZ = HSZ + USZ;
+    __shared__ __align__(16) float lds[2 * BSZ];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int li = lane & 15, lg = lane >> 4, pair = wave >> 1, hh = wave & 1;
+    const int tr = 2 * pair + (li >> 3), tc = li & 7;
+    const int nch = a.cin / BK;
+    const long W = a.W;
+
+    struct Unit { int y0, x0, co0; };
+    auto unit_at = [&](int u) {
+        const unsigned uu = unsigned(u), xcd = uu & 7u, j = uu >> 3;
+        const unsigned q = j / unsigned(nb), sp = q * 8u + xcd;
+        Unit w;
+        w.co0 = int(j - q * unsigned(nb)) * CB;
+        const unsigned uy = sp / unsigned(tx);
+        w.y0 = int(sp) < spatial ? int(uy) * 8 : -1;
+        w.x0 = int(sp - uy * unsigned(tx)) * 16;
+        return w;
+    };
+    // Halo f4 number f = tid + 256 i of the 10 x 18 x 8 slice (f < 360): byte offset from the
+    // halo origin (y0 - 1, x0 - 1), fixed per thread; per unit it becomes NOFF (past the
+    // buffer range: the load returns zeros) where the pixel is outside the image.
+    constexpr int NOFF = int(0x80000000u);
+    int hfix[2], hgy[2], hgx[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int f = tid + 256 * i, px = f >> 1, hf = f & 1;
+        const int hy = px / HC, hx = px - hy * HC;
+        hfix[i] = ((hy * int(a.W) + hx) * int(a.ldi) + hf * 4) * 4;
+        hgy[i] = f < HR * HC * 2 ? hy : -1000000;
+        hgx[i] = hx;
+    }
+    auto halo_offsets = [&](const Unit& w, int (&ho)[2]) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int gy = w.y0 - 1 + hgy[i], gx = w.x0 - 1 + hgx[i];
+            bool ok = w.y0 >= 0 && gy >= 0 && gy < a.H && gx >= 0 && gx < a.W;
+            if constexpr (BATCH) {
+                if ((hgy[i] == 0 && w.y0 % a.img_h == 0) || (hgy[i] == HR - 1 && (w.y0 + 8) % a.img_h == 0)) ok = false;
+            }
+            ho[i] = ok ? hfix[i] : NOFF;
+        }
+    };
+    // Filter slice: f4 number f = tid + 256 i is row r = f >> 1 = (tid >> 1) + 128 i of the
+    // [16 xi][CB co] x 8 ci slice, half tid & 1; byte offset fixed per thread plus i * ustep.
+    const int uoff = ((((tid >> 1) / CB) * a.cout + ((tid >> 1) % CB)) * BK + (tid & 1) * 4) * 4;
+    const int ustep = (128 / CB) * a.cout * BK * 4;
+    f4 rh[2], ru[NU];
+    auto load = [&](const Unit& w, const int (&ho)[2], int cs) {
+        const float* hb = a.in + ((long(w.y0) - 1) * W + (w.x0 - 1)) * a.ldi + cs * BK;
+        const rsrc_t hr = rsrc(hb);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) rh[i] = bld4(hr, ho[i], 0);
+        const rsrc_t ur = rsrc(a.w8 + (long(cs) * 16 * a.cout + w.co0) * BK);
+#pragma unroll
+        for (int i = 0; i < NU; ++i) ru[i] = bld4(ur, uoff, i * ustep);
+    };
+    // LDS stash bases (floats), fixed per thread: halo pixel (tid >> 1) + 128 i; filter row
+    // (tid >> 1) + 128 i with its 8-byte slots XOR-swizzled by g = (row >> 2) & 3, which is
+    // (tid >> 3) & 3 for every i.
+    const int hl = (tid >> 1) * PP + (tid & 1) * 4;
+    const int ug = (tid >> 3) & 3;
+    const int ul0 = (tid >> 1) * 8 + 2 * ((2 * (tid & 1)) ^ ug);
+    const int ul1 = (tid >> 1) * 8 + 2 * ((2 * (tid & 1) + 1) ^ ug);
+    const bool h2nd = tid + 256 < HR * HC * 2;
+    auto stash = [&](float* buf) {
+        st2(buf + hl, f2{rh[0][0], rh[0][1]});
+        st2(buf + hl + 2, f2{rh[0][2], rh[0][3]});
+        if (h2nd) {
+            st2(buf + hl + 128 * PP, f2{rh[1][0], rh[1][1]});
+            st2(buf + hl + 128 * PP + 2, f2{rh[1][2], rh[1][3]});
+        }
+        float* us = buf + HSZ;
+#pragma unroll
+        for (int i = 0; i < NU; ++i) {
+            st2(us + ul0 + i * 1024, f2{ru[i][0], ru[i][1]});
+            st2(us + ul1 + i * 1024, f2{ru[i][2], ru[i][3]});
+        }
+    };
+    const int gread = (li >> 2) & 3;
+    const int pbase = ((2 * tr + hh) * HC + 2 * tc) * PP + 2 * lg;
+    f4 acc[NCB][2][4];
+    auto slice = [&](auto HHc, auto FIRSTc, const float* buf) {
+        constexpr int H2 = decltype(HHc)::value;
+        constexpr bool FIRST = decltype(FIRSTc)::value;
+        const float* Us = buf + HSZ + li * 8 + 2 * (lg ^ gread);
+        f2 t[2][4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float* col = buf + pbase + j * PP;
+            const f2 da = ld2(col), db = ld2(col + HC * PP), dc = ld2(col + 2 * HC * PP);
+            if constexpr (H2 == 0) {
+                t[0][j] = da - dc;
+                t[1][j] = db + dc;
+            } else {
+                t[0][j] = db - da;
+                t[1][j] = da - dc;
+            }
+        }
+#pragma unroll
+        for (int ii = 0; ii < 2; ++ii) {
+            const f2 v[4] = {t[ii][0] - t[ii][2], t[ii][1] + t[ii][2], t[ii][2] - t[ii][1], t[ii][1] - t[ii][3]};
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int cb = 0; cb < NCB; ++cb) {
+                    const int r = ((2 * H2 + ii) * 4 + j) * CB + cb * 16;
+                    const f2 uu = ld2(Us + r * 8);
+                    acc[cb][ii][j] = mfma4(uu[0], v[j][0], FIRST ? f4{0.f, 0.f, 0.f, 0.f} : acc[cb][ii][j]);
+                    acc[cb][ii][j] = mfma4(uu[1], v[j][1], acc[cb][ii][j]);
+                }
+        }
+    };
+    // Each wave keeps NCB / 2 of its channel blocks (the ones of half hh) and hands the other
+    // half's partial outputs to its partner through LDS.
+    constexpr int NK = NCB / 2;
+    auto finish = [&](auto HHc, const Unit& w, float* xb) {
+        constexpr int H2 = decltype(HHc)::value;
+        f4 yp[NCB][2][2];
+#pragma unroll
+        for (int cb = 0; cb < NCB; ++cb) {
+            f4 r[2][2];
+#pragma unroll
+            for (int ii = 0; ii < 2; ++ii) {
+                r[ii][0] = acc[cb][ii][0] + acc[cb][ii][1] + acc[cb][ii][2];
+                r[ii][1] = acc[cb][ii][1] - acc[cb][ii][2] - acc[cb][ii][3];
+            }
+#pragma unroll
+            for (int b = 0; b < 2; ++b) {
+                if constexpr (H2 == 0) {
+                    yp[cb][0][b] = r[0][b] + r[1][b];
+                    yp[cb][1][b] = r[1][b];
+                } else {
+                    yp[cb][0][b] = r[0][b];
+                    yp[cb][1][b] = f4{0.f, 0.f, 0.f, 0.f} - r[0][b] - r[1][b];
+                }
+            }
+        }
+        float* xo = xb + ((wave ^ 1) * 64 + lane) * 16 * NK;
+#pragma unroll
+        for (int k = 0; k < NK; ++k)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) st4(xo + 16 * k + 4 * ((q + lane) & 3), yp[(1 - H2) * NK + k][q >> 1][q & 1]);
+        __syncthreads();
+        const float* xi = xb + (wave * 64 + lane) * 16 * NK;
+        f4 got[NK][4];
+#pragma unroll
+        for (int k = 0; k < NK; ++k)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) got[k][q] = ld4(xi + 16 * k + 4 * ((q + lane) & 3));
+        __syncthreads();
+        if (w.y0 < 0) return;
+#pragma unroll
+        for (int k = 0; k < NK; ++k) {
+            const int co = w.co0 + (H2 * NK + k) * 16 + lg * 4;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int a0 = q >> 1, b = q & 1;
+                const int y = w.y0 + 2 * tr + a0, x = w.x0 + 2 * tc + b;
+                if (y >= a.H || x >= a.W) continue;
+                f4 v = yp[H2 * NK + k][a0][b] + got[k][q];
+                float* o = a.out + (long(y) * W + x) * a.ldo + co;
+                if constexpr (RELU) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) v[e] = fmaxf(v[e], 0.0f);
+                    st4(o, v);
+                } else {
+                    st4(o, ld4(o) + v);
+                }
+            }
+        }
+    };
+
+    int u = blockIdx.x;
+    if (u >= units) return;
+    Unit cur = unit_at(u);
+    int hcur[2], hnxt[2];
+    halo_offsets(cur, hcur);
+    load(cur, hcur, 0);
+    stash(lds);
+    __syncthreads();
+    int kb = 0;
+    for (;;) {
+        const int un = u + int(gridDim.x);
+        const Unit nxt = unit_at(un < units ? un : u);
+        halo_offsets(nxt, hnxt);
+        for (int c = 0; c < nch; ++c) {
+            const bool more = c + 1 < nch || un < units;
+            if (c + 1 < nch) load(cur, hcur, c + 1);
+            else if (un < units) load(nxt, hnxt, 0);
+            const float* buf = lds + kb * BSZ;
+            using I0 = std::integral_constant<int, 0>;
+            using I1 = std::integral_constant<int, 1>;
+            using T1 = std::integral_constant<bool, true>;
+            using T0 = std::integral_constant<bool, false>;
+            if (c == 0) {
+                if (hh == 0) slice(I0{}, T1{}, buf);
+                else slice(I1{}, T1{}, buf);
+            } else {
+                if (hh == 0) slice(I0{}, T0{}, buf);
+                else slice(I1{}, T0{}, buf);
+            }
+            if (more) stash(lds + (kb ^ 1) * BSZ);
+            __syncthreads();
+            kb ^= 1;
+        }
+        // The last slice's buffer (kb ^ 1) is free: its filter part takes the exchange.
+        float* xb = lds + (kb ^ 1) * BSZ + HSZ;
+        if (hh == 0) finish(std::integral_constant<int, 0>{}, cur, xb);
+        else finish(std::integral_constant<int, 1>{}, cur, xb);
+        if (un >= units) break;
+        u = un;
+        cur = nxt;
+        hcur[0] = hnxt[0];
+        hcur[1] = hnxt[1];
+    }
+}
+
 template <bool BATCH>
 static bool launch_wino(const Conv3Args& a, bool relu, bool wide, bool ures, hipStream_t s, const char** why) {
     static std::atomic<int> cus_c[8] = {}, pc_c[8] = {};
@@ -1953,19 +2216,60 @@ static bool launch_wino(const Conv3Args& a, bool relu, bool wide, bool ures, hip
     return true;
 }
 
+template <int CB, bool BATCH>
+static bool launch_wino3(const Conv3Args& a, bool relu, hipStream_t s, const char** why) {
+    static std::atomic<int> cus_c[2] = {}, pc_c[2] = {};
+    const int tx = (a.W + 15) / 16, ty = (a.H + 7) / 8;
+    const long spatial = long(tx) * ty, nb = a.cout / CB;
+    const long units = ((spatial + 7) / 8) * 8 * nb;
+    if (units >= (1L << 31)) {
+        *why = "conv3x3_winograd: more than 2^31 units";
+        return false;
+    }
+    Occ oc;
+    if (!query_occ(relu ? k_wino3<CB, true, BATCH> : k_wino3<CB, false, BATCH>, 256, cus_c[relu ? 1 : 0],
+                   pc_c[relu ? 1 : 0], &oc)) {
+        *why = "conv3x3_winograd: device query failed";
+        return false;
+    }
+    const unsigned grid = unsigned(std::min<long>(units, long(oc.cus) * oc.per_cu));
+    if (relu)
+        hipLaunchKernelGGL((k_wino3<CB, true, BATCH>), dim3(grid), dim3(256), 0, s, a, tx, int(nb), int(spatial),
+                           int(units));
+    else
+        hipLaunchKernelGGL((k_wino3<CB, false, BATCH>), dim3(grid), dim3(256), 0, s, a, tx, int(nb), int(spatial),
+                           int(units));
+    return true;
+}
+
 bool conv3x3_winograd(const Conv3Args& a, bool relu, hipStream_t s, const char** why) {
     if (a.cin % 16 != 0 || a.cout % 16 != 0 || (a.H & 1) || (a.W & 1)) {
         *why = "conv3x3_winograd: cin and cout must be multiples of 16 and the plane even";
         return false;
     }
-    if (double(a.H) * a.W * a.ldi >= 4294967296.0 || double(a.H) * a.W * a.ldo >= 4294967296.0 ||
-        double(a.cout) * a.cin * 16 >= 4294967296.0) {
-        *why = "conv3x3_winograd: plane too large for 32-bit element offsets";
-        return false;
-    }
     const bool batch = a.img_h > 0 && a.img_h < a.H;
     if (batch && ((a.img_h & 1) || a.H % a.img_h != 0)) {
         *why = "conv3x3_winograd: stacked images must have an even height that divides the plane";
+        return false;
+    }
+    // k_wino3 (64-bit unit bases, 32-bit in-unit byte offsets: 10 halo rows of the plane must
+    // span less than 2^31 bytes; stacked images in units of 8 rows) at 64 or more output
+    // channels, where it is the fastest form; k_wino2 / k_wino (32-bit element offsets)
+    // elsewhere, and k_wino3 with 32-channel units for planes past 2^32 elements.
+    const bool fits32 = double(a.H) * a.W * a.ldi < 4294967296.0 && double(a.H) * a.W * a.ldo < 4294967296.0 &&
+                        double(a.cout) * a.cin * 16 < 4294967296.0;
+    const bool k3 = a.w8 && a.cblock == 0 && a.cin % 8 == 0 && a.cout % 32 == 0 &&
+                    10.0 * a.W * a.ldi * 4 < 2147483648.0 && (!batch || a.img_h % 8 == 0);
+    if (k3 && a.wino3 && ((a.cin >= 64 && a.cout % 64 == 0) || a.wino3 == 2)) {
+        if (a.cout % 64 == 0)
+            return batch ? launch_wino3<64, true>(a, relu, s, why) : launch_wino3<64, false>(a, relu, s, why);
+        return batch ? launch_wino3<32, true>(a, relu, s, why) : launch_wino3<32, false>(a, relu, s, why);
+    }
+    if (!fits32) {
+        if (k3 && a.cout % 64 == 0)
+            return batch ? launch_wino3<64, true>(a, relu, s, why) : launch_wino3<64, false>(a, relu, s, why);
+        if (k3) return batch ? launch_wino3<32, true>(a, relu, s, why) : launch_wino3<32, false>(a, relu, s, why);
+        *why = "conv3x3_winograd: plane too large for 32-bit element offsets";
         return false;
     }
     // 32 output channels per unit, except at cin >= 256 (level 3 of the forward), where the
@@ -2141,6 +2445,13 @@ void winograd_filter(const float* g, int cout, int cin, float* u) {
                     u[(long(i * 4 + j) * cout + o) * cin + c] =
                         float(t[i][0] * G[j][0] + t[i][1] * G[j][1] + t[i][2] * G[j][2]);
         }
+}
+
+void winograd_filter_slices(const float* u, int cout, int cin, float* u8) {
+    for (int xi = 0; xi < 16; ++xi)
+        for (int o = 0; o < cout; ++o)
+            for (int c = 0; c < cin; ++c)
+                u8[((long(c / 8) * 16 + xi) * cout + o) * 8 + c % 8] = u[(long(xi) * cout + o) * cin + c];
 }
 
 // ---------------------------------------------------------------------------

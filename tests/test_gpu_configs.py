@@ -184,35 +184,47 @@ def _hip_with(weights_path, *envs):
 
 
 def test_direct_and_winograd_3x3_agree(weights_path, owt):
-    """The conv half's 3x3 convolutions by Winograd F(2x2,3x3) with 32 output channels per
-    unit (the default), with 16 (SCUNET_HIP_WINO16), with 16 in pairs of 8x16 half-tiles
-    (SCUNET_HIP_WINO_PAIR) and by the direct implicit GEMM (SCUNET_HIP_DIRECT3X3): all
-    against the oracle's cpu.rs conv3x3, op by op (planes that end in partial tiles and odd
-    half-tile counts included) and in a block."""
+    """The conv half's 3x3 convolutions by Winograd F(2x2,3x3) in every form: the default
+    (k_wino3 with 64-channel units from 64 channels up, k_wino2 with 32-channel units at 32),
+    k_wino3 everywhere (SCUNET_HIP_WINO3: 32-channel units at 32, the form large planes use),
+    the 32-bit-offset forms everywhere (SCUNET_HIP_WINO2), 16 channels per unit
+    (SCUNET_HIP_WINO16), 16 in pairs of 8x16 half-tiles (SCUNET_HIP_WINO_PAIR) and the direct
+    implicit GEMM (SCUNET_HIP_DIRECT3X3): all against the oracle's cpu.rs conv3x3, op by op
+    (planes that end in partial 8-row, 16-row and 16-column units, and odd half-tile counts)
+    and in a block."""
     from scunet_hip import Hip, synth
     direct = _hip_with(weights_path, "SCUNET_HIP_DIRECT3X3")
     w16 = _hip_with(weights_path, "SCUNET_HIP_WINO16")
     pair = _hip_with(weights_path, "SCUNET_HIP_WINO16", "SCUNET_HIP_WINO_PAIR")
+    w2 = _hip_with(weights_path, "SCUNET_HIP_WINO2")
+    w3 = _hip_with(weights_path, "SCUNET_HIP_WINO3")
     wino = Hip(weights_path)
+    forms = (("winograd", wino), ("wino3", w3), ("wino2", w2), ("winograd16", w16), ("pairs", pair),
+             ("direct", direct))
     try:
         for name, c, h, w in (("m_down1.0.conv_block.0", 32, 40, 24), ("m_down2.1.conv_block.2", 64, 16, 24),
                               ("m_down3.2.conv_block.0", 128, 24, 16), ("m_body.0.conv_block.2", 256, 16, 16),
-                              ("m_up1.2.conv_block.0", 32, 18, 34), ("m_up2.3.conv_block.2", 64, 50, 6)):
+                              ("m_up1.2.conv_block.0", 32, 18, 34), ("m_up2.3.conv_block.2", 64, 50, 6),
+                              ("m_up3.1.conv_block.0", 128, 26, 38), ("m_body.3.conv_block.0", 256, 10, 20)):
             x = synth.seq(c * h * w, 0.37).reshape(c, h, w)
             want = O.conv3x3(x, owt.t[name + ".weight"])
-            for tag, be in (("winograd", wino), ("winograd16", w16), ("pairs", pair), ("direct", direct)):
+            for tag, be in forms:
                 close(f"{tag} {name} {h}x{w}", want, be.op_probe("conv3x3", name, x, c, c, h, w), 1e-5)
-        for prefix, shift in (("m_down1.1", 4), ("m_body.2", 0)):
+        for prefix, shift in (("m_down1.1", 4), ("m_down2.2", 0), ("m_body.2", 0)):
             c = sum(owt.block_dims(prefix))
             x = synth.seq(c * 24 * 32, 0.61).reshape(c, 24, 32)
             want = O.conv_trans_block(owt, prefix, x, shift)
-            for be in (wino, w16, pair, direct):
+            for _, be in forms:
                 assert max_abs(want, be.block_dump(prefix, 24, 32, shift, x)) <= STAGE_TOL
+        # Whole forwards, stacked images included (units of 8 rows at the images' edges).
+        xs = np.stack([synth.noisy_image(50 + i, 3, 64, 64, 25) for i in range(3)])
+        for _, be in (("winograd", wino), ("wino3", w3)):
+            ys = be.run_batch(xs)
+            for i in range(3):
+                assert max_abs(O.run(owt, xs[i]), ys[i]) <= STAGE_TOL
     finally:
-        wino.close()
-        w16.close()
-        pair.close()
-        direct.close()
+        for _, be in forms:
+            be.close()
 
 
 def test_resident_chained_1x1_and_tiled_gemm_agree(weights_path, owt):
