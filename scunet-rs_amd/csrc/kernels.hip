@@ -2470,7 +2470,10 @@ void winograd_filter_slices(const float* u, int cout, int cin, float* u8) {
 // loads, 64 contiguous bytes per key), so the only LDS is the 7.2 KB of tables and the
 // kernel fits in 128 VGPRs: four waves per SIMD, 4 096 (window, head) units in flight.
 // ---------------------------------------------------------------------------
+template <bool WIDE>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4))) void k_attention(AttnArgs a, long units) {
+    // Element offsets: 32-bit (WIDE = false) unless the qkv plane reaches 2^32 elements.
+    using U = typename std::conditional<WIDE, unsigned long, unsigned>::type;
     __shared__ float rps[8 * 225];                // log2(e) * rel-pos tables, all heads
     for (int i = threadIdx.x; i < a.heads * 225; i += 256) rps[i] = a.tab[i];
     __syncthreads();                              // the only barrier
@@ -2489,36 +2492,36 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
     // 16nd + li of those 4 keys with 4-byte loads, 64 contiguous bytes per key and
     // instruction). In pixel mode token (ty, tx) of window (wh, ww) is pixel
     // ((8wh + ty + shift) mod H, (8ww + tx + shift) mod W) (cpu.rs:648-652's cyclic shift
-    // folded into the addressing); the launcher checks that every offset fits 32 bits.
-    unsigned off[4], vy[4], vx[4];
+    // folded into the addressing).
+    U off[4], vy[4], vx[4];
     if (a.pixel_mode) {
-        auto wy = [&](int ty) { int y = wh * 8 + ty + a.shift; return unsigned(y >= a.H ? y - a.H : y); };
-        auto wx = [&](int tx) { int x = ww * 8 + tx + a.shift; return unsigned(x >= a.W ? x - a.W : x); };
-        const unsigned xq = wx(li & 7);
+        auto wy = [&](int ty) { int y = wh * 8 + ty + a.shift; return U(y >= a.H ? y - a.H : y); };
+        auto wx = [&](int tx) { int x = ww * 8 + tx + a.shift; return U(x >= a.W ? x - a.W : x); };
+        const U xq = wx(li & 7);
 #pragma unroll
-        for (int m = 0; m < 4; ++m) off[m] = (wy(2 * m + (li >> 3)) * unsigned(a.W) + xq) * unsigned(a.ldq);
+        for (int m = 0; m < 4; ++m) off[m] = (wy(2 * m + (li >> 3)) * U(a.W) + xq) * U(a.ldq);
 #pragma unroll
-        for (int kt = 0; kt < 4; ++kt) vy[kt] = wy(2 * kt + (lg >> 1)) * unsigned(a.W);
+        for (int kt = 0; kt < 4; ++kt) vy[kt] = wy(2 * kt + (lg >> 1)) * U(a.W);
 #pragma unroll
         for (int r = 0; r < 4; ++r) vx[r] = wx(4 * (lg & 1) + r);
     } else {
 #pragma unroll
-        for (int m = 0; m < 4; ++m) off[m] = (unsigned(wi) * 64u + 16u * m + li) * unsigned(a.ldq);
+        for (int m = 0; m < 4; ++m) off[m] = (U(wi) * 64u + 16u * m + li) * U(a.ldq);
 #pragma unroll
-        for (int kt = 0; kt < 4; ++kt) vy[kt] = unsigned(wi) * 64u + 16u * kt + 4u * lg;
+        for (int kt = 0; kt < 4; ++kt) vy[kt] = U(wi) * 64u + 16u * kt + 4u * lg;
 #pragma unroll
         for (int r = 0; r < 4; ++r) vx[r] = r;
     }
     // Row (pixel or window-major token) of token 16m + li, recomputed where the outputs
     // are stored so that no register holds it through the products.
-    auto row_of = [&](int m) -> unsigned {
+    auto row_of = [&](int m) -> U {
         if (a.pixel_mode) {
             int y = wh * 8 + 2 * m + (li >> 3) + a.shift, x = ww * 8 + (li & 7) + a.shift;
             y = y >= a.H ? y - a.H : y;
             x = x >= a.W ? x - a.W : x;
-            return unsigned(y) * unsigned(a.W) + unsigned(x);
+            return U(y) * U(a.W) + U(x);
         }
-        return unsigned(wi) * 64u + 16u * m + li;
+        return U(wi) * 64u + 16u * m + li;
     };
     const float* q_base = a.qkv + hoff;
     const float* k_base = a.qkv + a.C + hoff;
@@ -2540,7 +2543,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
 #pragma unroll
         for (int nd = 0; nd < 2; ++nd)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) vv[kt][nd][r] = v_base[(vy[kt] + vx[r]) * unsigned(a.ldq) + 16 * nd];
+            for (int r = 0; r < 4; ++r) vv[kt][nd][r] = v_base[(vy[kt] + vx[r]) * U(a.ldq) + 16 * nd];
     // Bias: query p = 16nt + li and key q = 16mt + 4lg + r give table entry
     // (p/8 - q/8 + 7) * 15 + (p%8 - q%8 + 7) = base + 30 (nt - mt) - r (cpu.rs:532-546);
     // read from LDS where each logit is formed.
@@ -2617,13 +2620,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
 bool attention(const AttnArgs& a, hipStream_t s, const char** why) {
     if (a.C != a.heads * 32) { *why = "attention: head_dim must be 32"; return false; }
     const double rows = a.pixel_mode ? double(a.H) * a.W : double(a.nwh) * a.nww * 64.0;
-    if (rows * double(a.ldq) >= 4294967296.0) { *why = "attention: qkv plane too large for 32-bit offsets"; return false; }
+    // 32-bit element offsets while the qkv and output planes allow (the measured form), else 64-bit.
+    const bool wide = a.wide || rows * double(a.ldq) >= 4294967296.0 || rows * double(a.ldo) >= 4294967296.0;
     if (a.shift != 0 && a.shift != 4) { *why = "attention: the shifted-window mask assumes shift 4"; return false; }
     if (a.heads > 8) { *why = "attention: at most 8 heads"; return false; }
     long units = long(a.nwh) * a.nww * a.heads;
     if (units == 0) return true;
     dim3 grid(unsigned((units + 3) / 4));
-    hipLaunchKernelGGL(k_attention, grid, dim3(256), 0, s, a, units);
+    if (wide) hipLaunchKernelGGL(k_attention<true>, grid, dim3(256), 0, s, a, units);
+    else hipLaunchKernelGGL(k_attention<false>, grid, dim3(256), 0, s, a, units);
     return true;
 }
 

@@ -74,6 +74,36 @@ def test_fused_and_three_launch_attention_halves_agree(weights_path, owt):
         unf.close()
 
 
+def test_attention_64bit_offsets_form_agrees(weights_path, owt):
+    """The attention kernel's 64-bit-offset form (what planes of 2^32 qkv elements or more
+    take; SCUNET_HIP_ATTN64 selects it at every size) against its 32-bit form: the same bits,
+    in window-major mode (the kernel probe) and in pixel mode with the cyclic roll (the
+    three-launch attention half of a block)."""
+    from scunet_hip import synth
+    wide = _hip_with(weights_path, "SCUNET_HIP_ATTN64")
+    wide_unf = _hip_with(weights_path, "SCUNET_HIP_ATTN64", "SCUNET_HIP_UNFUSED_MSA")
+    narrow_unf = _hip_with(weights_path, "SCUNET_HIP_UNFUSED_MSA")
+    narrow = _hip_with(weights_path)
+    try:
+        rng = np.random.default_rng(77)
+        for c, (hh, ww) in ((32, (24, 40)), (128, (16, 32)), (256, (16, 16))):
+            heads = c // 32
+            qkv = rng.standard_normal(((hh // 8) * (ww // 8) * 64, 3 * c), dtype=np.float32)
+            rp = (rng.standard_normal((heads, 15, 15)) * 0.02).astype(np.float32)
+            for shift in (0, 4):
+                a = narrow.attention_kernel_probe(hh, ww, c, heads, 32, shift, qkv, rp)
+                b = wide.attention_kernel_probe(hh, ww, c, heads, 32, shift, qkv, rp)
+                assert np.array_equal(a, b), (c, shift)
+        for prefix, h, w, shift in (("m_down1.1", 24, 40, 4), ("m_up3.2", 16, 40, 0), ("m_body.1", 24, 24, 4)):
+            c = sum(owt.block_dims(prefix))
+            x = synth.seq(c * h * w, 0.59).reshape(c, h, w)
+            assert np.array_equal(narrow_unf.block_dump(prefix, h, w, shift, x),
+                                  wide_unf.block_dump(prefix, h, w, shift, x)), prefix
+    finally:
+        for be in (wide, wide_unf, narrow_unf, narrow):
+            be.close()
+
+
 def _attn_windows_f64(qkv, rp, nwh, nww, c, heads, shift, wins):
     cord = np.array([[i, j] for i in range(8) for j in range(8)])
     rel = cord[:, None, :] - cord[None, :, :] + 7
@@ -413,35 +443,145 @@ def test_run_batch_fp16_equals_single_runs(weights_path):
             assert np.array_equal(ys[i], be.run_fused(xs[i])), i
 
 
-def test_config4_gray_4096_full_size(weights_path_gray):
-    """benchmark config 4 at its real size, 1x1x4096x4096 (the size whose unfused hidden
-    layer passes 2^31 elements): the whole forward is finite, bit-identical on repeat, and the
-    device pad/crop path equals the plain forward (4096 needs no padding). One level-0
-    ConvTransBlock over the full 4096^2 plane (64 channels, both window phases) is checked
-    against the oracle on a middle band: the block is local (two 3x3 convolutions, 8x8
-    windows aligned to the plane, the cyclic roll and its mask acting only at the plane's
-    edges), so output rows 16 or more away from the band's cut see exactly what they see in
-    the full plane."""
-    from scunet_hip import Hip, Plan, synth
-    owt = O.Weights.load(weights_path_gray)
+def _say(*a):
+    print(*a, flush=True)
+
+
+def _band_check_block(be, ow, prefix, c, hh, ww, rows, seed, margin=16):
+    """One ConvTransBlock over a whole hh x ww plane through the device, against the oracle on
+    the band `rows` (both window phases). The block is local: two 3x3 convolutions, 8x8
+    windows aligned to the plane, and the cyclic roll with its mask acting only at the plane's
+    edges, so output rows `margin` or more away from the cut of a band with that margin see
+    exactly what they see in the full plane."""
+    r0, r1 = rows
+    rng = np.random.default_rng(seed)
+    xb = rng.standard_normal((c, hh, ww), dtype=np.float32)
+    band = np.ascontiguousarray(xb[:, r0 - margin:r1 + margin])
+    for shift in (0, 4):
+        got = be.block_dump(prefix, hh, ww, shift, xb)
+        want = O.conv_trans_block(ow, prefix, band, shift)[:, margin:-margin]
+        d = max_abs(want, got[:, r0:r1])
+        _say(f"  block {prefix} {hh}x{ww} shift {shift}: max |gpu - cpu| on rows {r0}-{r1} = {d:.2e}")
+        assert d <= STAGE_TOL, (prefix, shift, d)
+        assert np.isfinite(got[:, ::97, ::89]).all()
+        del got
+
+
+def test_config4_gray_4096_stages_on_bands(weights_path_gray):
+    """Benchmark config 4 at its real size, 1x1x4096x4096 (its level-0 planes hold 2^30
+    floats, the unfused hidden layer 2^31). The whole forward through forward_dump (every
+    stage plane copied out) equals scunet_hip_run bit for bit and is finite; then every local
+    operator of the walker is checked against the oracle on a middle row band of the planes
+    the device produced (cpu.rs:1175-1321): m_head from the input, each stride-2 down
+    convolution (m_downK from m_downK_blocks), each transposed up convolution with its skip
+    join (m_upK_up from the level below plus the skip), m_tail_in (m_up1 plus the head
+    recomputed) and m_tail; and one ConvTransBlock of every level over its whole plane."""
+    from scunet_hip import Hip, synth
+    ow = O.Weights.load(weights_path_gray)
     x = synth.config_input(4)
     assert x.shape == (1, 4096, 4096)
+    H = 4096
+    # Row bands per level k (plane height 4096 >> k): [c0 >> k, c1 >> k) plus a margin of 2
+    # rows either side (the 3x3 convolutions need 1; the 2x2 ones need the paired rows).
+    c0, c1, m = 2048, 2176, 2
+    keep = {}
+
+    def hook(name, v):
+        lvl = {"m_head": 0, "m_down1_blocks": 0, "m_down1": 1, "m_down2_blocks": 1, "m_down2": 2,
+               "m_down3_blocks": 2, "m_down3": 3, "m_body": 3, "m_up3_up": 2, "m_up3": 2, "m_up2_up": 1,
+               "m_up2": 1, "m_up1_up": 0, "m_up1": 0, "m_tail_in": 0, "m_tail": 0}[name]
+        h = H >> lvl
+        plane = v.reshape(-1, h, h)
+        keep[name] = np.ascontiguousarray(plane[:, (c0 >> lvl) - m:(c1 >> lvl) + m])
+
     with Hip(weights_path_gray) as be:
+        _say("config 4: forward_dump at 4096x4096")
+        y = be.forward_dump(x, hook)
+        assert np.isfinite(y).all()
+        assert 0.0 < float(np.abs(y).mean()) < 10.0
+        assert np.array_equal(y, be.run_fused(x))
+        assert sorted(keep) == sorted(["m_head", "m_down1_blocks", "m_down1", "m_down2_blocks", "m_down2",
+                                       "m_down3_blocks", "m_down3", "m_body", "m_up3_up", "m_up3", "m_up2_up",
+                                       "m_up2", "m_up1_up", "m_up1", "m_tail_in", "m_tail"])
+
+        def interior(a, lvl):     # the band [c0, c1) of a kept plane at level lvl
+            return a[:, m:m + ((c1 - c0) >> lvl)]
+
+        xb = np.ascontiguousarray(x[:, c0 - m:c1 + m])
+        head = O.conv3x3(xb, ow.t["m_head.0.weight"])
+        checks = {"m_head": max_abs(interior(head, 0), interior(keep["m_head"], 0))}
+        for k in range(3):
+            src, dst = keep[f"m_down{k + 1}_blocks"], keep[f"m_down{k + 1}"]
+            # m_downK band rows [c0 >> (k+1), c1 >> (k+1)) come from source rows [c0 >> k, c1 >> k).
+            s = np.ascontiguousarray(src[:, m:m + ((c1 - c0) >> k)])
+            got = O.conv2x2s2(s, ow.t[f"m_down{k + 1}.4.weight"])
+            checks[f"m_down{k + 1}"] = max_abs(got, interior(dst, k + 1))
+        for name, below, skip, lvl in (("up3", "m_body", "m_down3", 2), ("up2", "m_up3", "m_down2", 1),
+                                       ("up1", "m_up2", "m_down1", 0)):
+            # m_upK_up band rows [c0 >> lvl, c1 >> lvl) come from rows [c0 >> (lvl+1), c1 >> (lvl+1)).
+            s = interior(keep[below], lvl + 1) + interior(keep[skip], lvl + 1)
+            got = O.conv_t2x2(np.ascontiguousarray(s), ow.t[f"m_{name}.0.weight"])
+            checks[f"m_{name}_up"] = max_abs(got, interior(keep[f"m_{name}_up"], lvl))
+        checks["m_tail_in"] = max_abs(interior(keep["m_up1"] + head, 0), interior(keep["m_tail_in"], 0))
+        tail = O.conv3x3(keep["m_tail_in"], ow.t["m_tail.0.weight"])
+        checks["m_tail"] = max_abs(interior(tail, 0), interior(keep["m_tail"], 0))
+        checks["output"] = max_abs(interior(keep["m_tail"], 0), y[:, c0:c1])
+        _say("config 4 band checks, max |gpu - cpu|:", {k: f"{v:.2e}" for k, v in checks.items()})
+        assert all(d <= STAGE_TOL for d in checks.values()), checks
+        keep.clear()
+        # One ConvTransBlock per level over its whole 4096 >> k plane (level 0 is 2^30 floats).
+        for prefix, lvl in (("m_down1.1", 0), ("m_down2.0", 1), ("m_down3.3", 2), ("m_body.1", 3)):
+            h = H >> lvl
+            c = sum(ow.block_dims(prefix))
+            _band_check_block(be, ow, prefix, c, h, h, (h // 2, h // 2 + 64), 44 + lvl)
+
+
+def test_planes_past_2_32_elements(weights_path, weights_path_gray):
+    """Planes past 2^32 elements (64-bit unit bases in the Winograd 3x3, 64-bit row offsets
+    elsewhere). An 8192x8192 colour image: its level-0 planes hold exactly 2^32 floats; the
+    forward is finite, bit-identical on repeat and through the plain forward (8192 needs no
+    padding). Four 4096x4096 gray images stacked (scunet_hip_run_batch, level-0 plane 2^32
+    floats) give each image's own forward bit for bit when the single runs use the same
+    (64-bit) Winograd form. One level-0 ConvTransBlock over an
+    8192x8256 plane (64 x 8192 x 8256 = 2^32 + 2^26 floats) against the oracle on a middle
+    band."""
+    from scunet_hip import Hip, Plan, synth
+    with Hip(weights_path) as be:
+        _say("8192x8192 colour: input")
+        x = synth.noisy_image(105, 3, 8192, 8192, 15)
+        _say("8192x8192 colour: forwards")
         a = be.run_fused(x)
         assert np.isfinite(a).all()
-        assert np.array_equal(a, be.run_fused(x))
-        assert np.array_equal(a, be.forward(x, Plan(4096, 4096)))
         assert 0.0 < float(np.abs(a).mean()) < 10.0
-        c = sum(owt.block_dims("m_down1.1"))
-        rng = np.random.default_rng(44)
-        xb = rng.standard_normal((c, 4096, 4096), dtype=np.float32)
-        r0, r1, m = 1984, 2112, 16
-        for shift in (0, 4):
-            got = be.block_dump("m_down1.1", 4096, 4096, shift, xb)
-            band = np.ascontiguousarray(xb[:, r0 - m:r1 + m])
-            want = O.conv_trans_block(owt, "m_down1.1", band, shift)[:, m:-m]
-            assert max_abs(want, got[:, r0:r1]) <= STAGE_TOL, shift
-            assert np.isfinite(got).all()
+        assert np.array_equal(a, be.run_fused(x))
+        assert np.array_equal(a, be.forward(x, Plan(8192, 8192)))
+        del a, x
+        ow = O.Weights.load(weights_path)
+        _say("8192x8256 level-0 block")
+        # Rows 8136-8167 start at pixel 8136 * 8256 = 2^26 + 61952: element offsets past 2^32.
+        # The band (8120-8184 with its margins) stays clear of the last window row, whose
+        # shifted windows wrap around to the top of the plane.
+        _band_check_block(be, ow, "m_up1.2", 64, 8192, 8256, (8136, 8168), 46)
+        be.release_scratch()
+    # The stacked plane (2^32 floats at level 0) takes the 64-bit Winograd form at every
+    # level, which sums the input channels in slices of 8: the single-image references run
+    # with that form forced (SCUNET_HIP_WINO3), and the default handle agrees to rounding.
+    os.environ["SCUNET_HIP_WINO3"] = "1"
+    try:
+        single = Hip(weights_path_gray)
+    finally:
+        del os.environ["SCUNET_HIP_WINO3"]
+    try:
+        with Hip(weights_path_gray) as be:
+            _say("4 x 4096x4096 gray stacked")
+            xs = np.stack([synth.noisy_image(106 + i, 1, 4096, 4096, 25) for i in range(4)])
+            ys = be.run_batch(xs)
+            assert np.isfinite(ys).all()
+            for i in range(4):
+                assert np.array_equal(ys[i], single.run_fused(xs[i])), i
+            assert max_abs(be.run_fused(xs[0]), ys[0]) <= 1e-5
+    finally:
+        single.close()
 
 
 def test_two_handles_on_two_threads(weights_path):
