@@ -285,6 +285,11 @@ bool upload_weights(scunet_hip* h) {
         }
         host.push_back({n, std::move(v)});
     }
+    {
+        std::vector<float> gt(GELU_TABLE);
+        build_gelu_table(gt.data());
+        host.push_back({"@gelu", std::move(gt)});
+    }
     size_t total = 0;
     for (auto& e : host) total += (e.second.size() * 4 + 255) / 256 * 256;
     void* p = nullptr;
@@ -297,7 +302,7 @@ bool upload_weights(scunet_hip* h) {
             return false;
         if (e.first.rfind("@tab:", 0) == 0) h->tab[e.first.substr(5)] = reinterpret_cast<float*>(at);
         else if (e.first.rfind("@atab:", 0) == 0) h->atab[e.first.substr(6)] = reinterpret_cast<float*>(at);
-        else h->w[e.first] = reinterpret_cast<float*>(at);   // "@wino:" / "@wino8:" are Winograd filters
+        else h->w[e.first] = reinterpret_cast<float*>(at);   // "@wino:" / "@wino8:" Winograd filters, "@gelu"
         at += (e.second.size() * 4 + 255) / 256 * 256;
     }
     return true;
@@ -508,6 +513,7 @@ bool block(scunet_hip* h, const std::string& p, float* x, int H, int Wd, int shi
             m.w0 = W(h, tp + ".mlp.0.weight"); m.b0 = W(h, tp + ".mlp.0.bias");
             m.w2 = W(h, tp + ".mlp.2.weight"); m.b2 = W(h, tp + ".mlp.2.bias");
             m.h0 = W16(h, tp + ".mlp.0.weight"); m.h2 = W16(h, tp + ".mlp.2.weight");
+            m.gelu = W(h, "@gelu");
         }
         const double nw = double(m.nwh) * m.nww * nimg;
         const double msa_flop = 64.0 * nw * (8.0 * t * t) + 16384.0 * t * nw;
@@ -525,6 +531,7 @@ bool block(scunet_hip* h, const std::string& p, float* x, int H, int Wd, int shi
         m.w0 = W(h, tp + ".mlp.0.weight"); m.b0 = W(h, tp + ".mlp.0.bias");
         m.w2 = W(h, tp + ".mlp.2.weight"); m.b2 = W(h, tp + ".mlp.2.bias"); m.M = P; m.t = t;
         m.h0 = W16(h, tp + ".mlp.0.weight"); m.h2 = W16(h, tp + ".mlp.2.weight");
+        m.gelu = W(h, "@gelu");
         Span sp(h, "mlp_fused", mlp_flop, 4.0 * (2.0 * P * t + 8.0 * t * t + 5.0 * t));
         const char* why = nullptr;
         if (!mlp(m, h->stream, &why)) return fail(h, why);

@@ -108,10 +108,24 @@ struct MlpArgs {
     const float* b2 = nullptr;     // [t]
     const half_t* h0 = nullptr;    // fp16 mode: W0, W2 k-permuted
     const half_t* h2 = nullptr;
+    const float* gelu = nullptr;   // the GELU table (build_gelu_table), GELU_TABLE floats
     long M = 0;
     int t = 0;
 };
 bool mlp(const MlpArgs& a, hipStream_t s, const char** why);
+
+// GELU as the fused kernels evaluate it: Phi(v) = (1 + erf(v / sqrt 2)) / 2 with the
+// reference's Abramowitz & Stegun 7.1.26 erf (cpu.rs:318-332), tabulated in double on the
+// host as GELU_PIECES cubic pieces of width 1/16 over [-6, 6) (coefficients a, b, c, d of
+// a + f (b + f (c + f d)), f the position in the piece), and gelu(v) = v Phi(v) with the
+// argument clamped to the table (Phi is within 1e-9 of 0 or 1 outside it). The table holds
+// the A&S function to 2e-8 of Phi; evaluated in fp32 the result is within 1.7e-7 |v| of the
+// A&S GELU. It replaces the fp32 A&S evaluation (two transcendental instructions and a
+// dozen VALU ones) by a 16-byte LDS read and a cubic: on gfx950 VALU work delays the fp32
+// matrix products it is interleaved with, and it bounds the fp16-mode window kernels.
+constexpr int GELU_PIECES = 192;
+constexpr int GELU_TABLE = 4 * GELU_PIECES;
+void build_gelu_table(float* tab);
 
 struct Conv3Args {
     const float* in = nullptr;
@@ -184,6 +198,7 @@ struct MsaArgs {
     const half_t* hp = nullptr;
     const half_t* h0 = nullptr;
     const half_t* h2 = nullptr;
+    const float* gelu = nullptr;   // with the MLP option: the GELU table (build_gelu_table)
     int t = 0;
     int nwh = 0, nww = 0, H = 0, W = 0, shift = 0;   // nwh, H: one image's window rows and rows
     int nimg = 1;                                     // images stacked along y

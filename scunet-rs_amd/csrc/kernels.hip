@@ -79,6 +79,19 @@ DEVI float gelu_as(float v) {
     return fmaf(-av, q, fmaxf(v, 0.0f));
 }
 
+// The table form of the same GELU (build_gelu_table): tab is the table in LDS.
+DEVI float gelu_lut(const float* tab, float v) {
+    const float u = fminf(fmaxf(fmaf(v, 16.0f, 96.0f), 0.0f), 191.99998f);   // piece index + fraction
+    const int i = int(u);
+    const float f = __builtin_amdgcn_fractf(u);
+    const f4 c = ld4(tab + 4 * i);
+    return v * fmaf(fmaf(fmaf(c.w, f, c.z), f, c.y), f, c.x);
+}
+// A workgroup copies the table from global memory into its LDS (callers sync before use).
+DEVI void load_gelu_table(float* tab, const float* g, int tid, int nthreads) {
+    for (int i = tid; i < GELU_TABLE / 4; i += nthreads) st4(tab + 4 * i, ld4(g + 4 * i));
+}
+
 // ---------------------------------------------------------------------------
 // GEMM: C[m][n] = epi(sum_k A[m][k] W[n][k] + bias[n]), M pixels, N and K small.
 // Tile BM x BN x 32, 256 threads = 4 waves, each wave WM x WN of 16x16 MFMA tiles.
@@ -1050,9 +1063,11 @@ __global__ __launch_bounds__(NWV * 64) void k_mlp(MlpArgs a) {
     static_assert(!H16 || HC % 32 == 0, "fp16 slices are whole 32-wide k blocks");
     using ET = std::conditional_t<H16, _Float16, float>;
     __shared__ __align__(16) ET lds[2 * BUF];
+    __shared__ __align__(16) float gtab[GELU_TABLE];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int li = lane & 15, lg = lane >> 4;
+    load_gelu_table(gtab, a.gelu, tid, NTH);
     const long row0 = long(blockIdx.x) * (16 * MT * NWV) + wave * 16 * MT;
 
     f4 xa[MT][KG];
@@ -1186,7 +1201,7 @@ __global__ __launch_bounds__(NWV * 64) void k_mlp(MlpArgs a) {
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-                for (int r = 0; r < 4; ++r) acc1[ht][mt][r] = gelu_as(acc1[ht][mt][r] + bb[r]);
+                for (int r = 0; r < 4; ++r) acc1[ht][mt][r] = gelu_lut(gtab, acc1[ht][mt][r] + bb[r]);
         }
         if constexpr (H16) {
 #pragma unroll
@@ -1232,6 +1247,10 @@ __global__ __launch_bounds__(NWV * 64) void k_mlp(MlpArgs a) {
 
 bool mlp(const MlpArgs& a, hipStream_t s, const char** why) {
     if (a.M <= 0) return true;
+    if (!a.gelu) {
+        *why = "mlp: no GELU table";
+        return false;
+    }
     auto go = [&](auto kern, int rows_per_block, int threads = 256) {
         dim3 grid{unsigned((a.M + rows_per_block - 1) / rows_per_block), 1u, 1u};
         dim3 block{unsigned(threads), 1u, 1u};
@@ -2447,6 +2466,28 @@ void winograd_filter(const float* g, int cout, int cin, float* u) {
         }
 }
 
+void build_gelu_table(float* tab) {
+    // Abramowitz & Stegun 7.1.26, the erf of cpu.rs:318-332, in double.
+    auto erf_as = [](double x) {
+        const double t = 1.0 / (1.0 + 0.3275911 * std::fabs(x));
+        const double y = 1.0 - (((((1.061405429 * t - 1.453152027) * t) + 1.421413741) * t - 0.284496736) * t +
+                                0.254829592) * t * std::exp(-x * x);
+        return x >= 0 ? y : -y;
+    };
+    auto phi = [&](double v) { return 0.5 * (1.0 + erf_as(v / std::sqrt(2.0))); };
+    for (int i = 0; i < GELU_PIECES; ++i) {
+        // The cubic through f = 0, 1/3, 2/3, 1 of the piece [x0, x0 + 1/16): forward
+        // differences in s = 3 f, expanded into powers of f.
+        const double x0 = -6.0 + i / 16.0, h = 1.0 / 16.0;
+        const double y0 = phi(x0), y1 = phi(x0 + h / 3), y2 = phi(x0 + 2 * h / 3), y3 = phi(x0 + h);
+        const double d1 = y1 - y0, d2 = y2 - 2 * y1 + y0, d3 = y3 - 3 * y2 + 3 * y1 - y0;
+        tab[4 * i + 0] = float(y0);
+        tab[4 * i + 1] = float(3.0 * (d1 - d2 / 2 + d3 / 3));
+        tab[4 * i + 2] = float(9.0 * (d2 / 2 - d3 / 2));
+        tab[4 * i + 3] = float(4.5 * d3);
+    }
+}
+
 void winograd_filter_slices(const float* u, int cout, int cin, float* u8) {
     for (int xi = 0; xi < 16; ++xi)
         for (int o = 0; o < cout; ++o)
@@ -2657,10 +2698,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(T == 32 ? 2
     constexpr int MLPF = MLP ? HID * P0 + T * P2 : 0;
     using ET = std::conditional_t<H16, _Float16, float>;
     __shared__ __align__(16) ET xs[4 * 64 * LDX + MLPF];
+    __shared__ __align__(16) float gtab[MLP ? GELU_TABLE : 4];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     ET* const wm0 = xs + 4 * 64 * LDX;
     ET* const wm2 = wm0 + HID * P0;
     if constexpr (MLP) {
+        load_gelu_table(gtab, a.gelu, threadIdx.x, 256);
         constexpr int EV = H16 ? 8 : 4;   // elements per 16-byte chunk
         const ET* g0 = H16 ? reinterpret_cast<const ET*>(a.h0) : reinterpret_cast<const ET*>(a.w0);
         const ET* g2 = H16 ? reinterpret_cast<const ET*>(a.h2) : reinterpret_cast<const ET*>(a.w2);
@@ -2994,7 +3037,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(T == 32 ? 2
 #pragma unroll
                 for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) acc1[ht][mt][r] = gelu_as(acc1[ht][mt][r] + bb[r]);
+                    for (int r = 0; r < 4; ++r) acc1[ht][mt][r] = gelu_lut(gtab, acc1[ht][mt][r] + bb[r]);
             }
             if constexpr (H16) {
                 // HC = 32 hidden units: k block ch of W2.
@@ -3059,10 +3102,12 @@ __global__ __launch_bounds__(T * 2) __attribute__((amdgpu_waves_per_eu(2, 2))) v
     static_assert(PH <= 2 * LDX, "fp16 rows fit the fp32 rows");
     __shared__ __align__(16) float xs[64 * LDX];   // normalised tokens [token][channel]
     __shared__ __align__(16) float os[64 * LDX];   // head outputs [token][head * 32 + dim]
+    __shared__ __align__(16) float gtab[MLP ? GELU_TABLE : 4];
     _Float16* const xsh = reinterpret_cast<_Float16*>(xs);
     _Float16* const osh = reinterpret_cast<_Float16*>(os);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int li = lane & 15, lg = lane >> 4;
+    if constexpr (MLP) load_gelu_table(gtab, a.gelu, threadIdx.x, T * 2);
     const long wi = blockIdx.x;
     // Window wi = (image, window row, window column); the roll wraps within the image.
     // Window counts fit 32 bits (the launch grid is 32-bit), so the divisions are 32-bit.
@@ -3414,7 +3459,7 @@ __global__ __launch_bounds__(T * 2) __attribute__((amdgpu_waves_per_eu(2, 2))) v
 #pragma unroll
                 for (int i = 0; i < MT; ++i)
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) acc1[ht][i][r] = gelu_as(acc1[ht][i][r] + bb[r]);
+                    for (int r = 0; r < 4; ++r) acc1[ht][i][r] = gelu_lut(gtab, acc1[ht][i][r] + bb[r]);
             }
             if constexpr (H16) {
                 // HC = 32 hidden units: k block ch of W2.
@@ -3470,6 +3515,10 @@ bool msa_fused(const MsaArgs& a, hipStream_t s, const char** why) {
     if (nw == 0) return true;
     if (a.w0 && a.t != 32 && a.t != 64) {
         *why = "msa_fused: the fused MLP is available at t = 32, 64";
+        return false;
+    }
+    if (a.w0 && !a.gelu) {
+        *why = "msa_fused: no GELU table";
         return false;
     }
     if (a.hqkv) {

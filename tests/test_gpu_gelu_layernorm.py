@@ -13,12 +13,14 @@ a crafted checkpoint whose blocks make one quantity appear at the block output:
 * LN2 (cpu.rs:800-805): proj = 0, mlp.0 = [I; 0] with bias 10 (GELU is the identity to fp32
   precision on [6, 14]), mlp.2 = [I | 0] with bias -10: the trans half is 2 x_t + LN2(x_t);
 * GELU (cpu.rs:293-332): x = 0, proj = 0, mlp.0 = 0 with chosen biases v, mlp.2 picks one hidden
-  unit per output channel: the trans half is exactly GELU(v) as the kernel evaluates it.
+  unit per output channel: the trans half is exactly GELU(v) as the kernel evaluates it (the
+  fused kernels read Phi from a cubic table of the A&S function, build_gelu_table).
 
 LayerNorm is compared with its closed form in float64 (two-pass variance, eps 1e-5, random
 affine); GELU with the exact 0.5 v (1 + erf(v / sqrt 2)) within the Abramowitz & Stegun 7.1.26
 bound the reference's CPU path carries (|erf error| < 1.5e-7) plus fp32 rounding, and with the
-oracle's own GELU (the reference's f64 A&S cast to f32) within fp32 rounding.
+oracle's own GELU (the reference's f64 A&S cast to f32) within the table's 1e-7 |v| plus fp32
+rounding (and 1e-9 |v| beyond +-6, where the table holds Phi at its ends).
 """
 import math
 
@@ -157,11 +159,14 @@ def test_gelu_against_erf(crafted, t, ln1, ln2, gelus):
             assert np.array_equal(got, np.repeat(got[:, :1], h * w, axis=1)), prefix
             g = got[:, 0].astype(np.float64)
             exact = np.array([0.5 * float(a) * (1.0 + math.erf(float(a) / math.sqrt(2.0))) for a in v])
-            # The kernel evaluates the A&S form in fp32 (hardware reciprocal and exp2, each within
-            # 1 ulp, a degree-5 polynomial): a few ulp of the result on top of the A&S bound.
+            # The kernels evaluate v Phi(v) from a cubic table of the A&S Phi (build_gelu_table):
+            # the fit and its fp32 evaluation hold Phi to 1e-7 (1e-7 |v| on GELU, plus rounding
+            # of the result), and beyond +-6 the table gives v Phi(+-6), Phi(-6) being ~1e-9.
+            av = np.abs(v.astype(np.float64))
             ulp = np.spacing(np.abs(exact).astype(np.float32)).astype(np.float64)
-            bound = 0.5 * np.abs(v.astype(np.float64)) * 1.5e-7 + 6.0 * ulp + 1e-9
+            table = 1e-7 * av + 4.0 * ulp + 1e-9 * np.maximum(1.0, av)
+            bound = 0.5 * av * 1.5e-7 + table
             assert (np.abs(g - exact) <= bound).all(), (prefix, float(np.abs(g - exact).max()))
             ref = O.gelu(v).astype(np.float64)                 # cpu.rs's A&S in f64, cast to f32
-            assert (np.abs(g - ref) <= 6.0 * ulp + 1e-9).all(), (prefix, float(np.abs(g - ref).max()))
+            assert (np.abs(g - ref) <= table).all(), (prefix, float(np.abs(g - ref).max()))
             assert np.array_equal(out[:t], np.zeros((t, h, w), np.float32))
