@@ -1048,7 +1048,7 @@ bool pconv(const PconvArgs& a, PconvMode mode, hipStream_t s, const char** why) 
 // H[row li][4 consecutive hidden units]: exactly the A operand of the second product, so
 // the hidden never goes through LDS or HBM. W0/W2 slices are double-buffered in LDS.
 // ---------------------------------------------------------------------------
-template <int T, int MT, int HC, bool H16, int NWV = 4>
+template <int T, int MT, int HC, bool H16, int NWV = 4, bool KEEP = true>
 __global__ __launch_bounds__(NWV * 64) void k_mlp(MlpArgs a) {
     constexpr int NTH = NWV * 64;
     constexpr int KG = T / 16, NT = T / 16, HT = HC / 16, NCH = 4 * T / HC;
@@ -1079,8 +1079,8 @@ __global__ __launch_bounds__(NWV * 64) void k_mlp(MlpArgs a) {
             xa[mt][kg] = r < a.M ? ld4(a.x + r * a.ldx + kg * 16 + lg * 4) : f4{0.f, 0.f, 0.f, 0.f};
     }
     // The raw rows stay in registers for the residual, unless they would crowd out the
-    // accumulators (then they are read again, from L2, at the end).
-    constexpr bool KEEPX = MT * KG <= 16;
+    // accumulators (then they are read again at the end).
+    constexpr bool KEEPX = KEEP && MT * KG <= 16;
     f4 xr[KEEPX ? MT : 1][KEEPX ? KG : 1];
     if constexpr (KEEPX) {
 #pragma unroll
@@ -1269,11 +1269,11 @@ bool mlp(const MlpArgs& a, hipStream_t s, const char** why) {
         // t = 128: 16 hidden units per slice (317 -> 314 us per launch at level 2 of 1080p).
         case 128: h16 ? go(k_mlp<128, 2, 32, true, 8>, 256, 512) : go(k_mlp<128, 1, 16, false>, 64); break;
         // fp32 at t = 256: 8 waves of one row tile each share every 32-unit weight slice
-        // (128 rows per workgroup; level 3 of 1080p: 337 -> 307 us per launch, against two
-        // row tiles per wave on 4 waves). Two waves per SIMD cap it at 256 VGPRs, so it
-        // spills 54 of them to scratch, which is in that time; the spill-free 4-wave shapes
-        // measured 337 us (two row tiles per wave) and 380 us (one).
-        case 256: h16 ? go(k_mlp<256, 2, 32, true>, 128) : go(k_mlp<256, 1, 32, false, 8>, 128, 512); break;
+        // (128 rows per workgroup; against two row tiles per wave on 4 waves 337 -> 307 us
+        // per launch at level 3 of 1080p). Two waves per SIMD cap it at 256 VGPRs: keeping
+        // the raw rows for the residual spilled 54 registers to scratch; reading the rows
+        // again at the end fits in 248 without a spill (312 -> 280 us, bit-identical).
+        case 256: h16 ? go(k_mlp<256, 2, 32, true>, 128) : go(k_mlp<256, 1, 32, false, 8, false>, 128, 512); break;
         default: *why = "mlp: t must be 32, 64, 128 or 256"; return false;
     }
     return true;
