@@ -101,6 +101,7 @@ struct scunet_hip {
     bool wino2 = false;                  // the 32-bit-offset Winograd forms wherever the plane allows
     bool wino3_all = false;              // k_wino3 at every level (32-channel units below 64 channels)
     bool attn64 = false;                 // the attention kernel with 64-bit offsets at every size
+    int attn_qs = 0;                     // the attention kernel's query parts (0: automatic)
     bool gemm2 = false;                  // one tile per workgroup GEMM (no persistent walker)
     bool gemm1x1 = false;                // the tiled GEMM for every 1x1 (no resident weights, no chaining)
     bool separate_mlp = false;           // the MLP as its own kernel also at t = 32
@@ -432,7 +433,7 @@ bool msa_unfused(scunet_hip* h, const std::string& p, float* yt, int c, int t, i
         AttnArgs a;
         a.qkv = s.qkv; a.ldq = 3 * t; a.out = s.o; a.ldo = t; a.tab = h->atab[p];
         a.C = t; a.heads = t / h->wt.head_dim; a.nwh = H / 8; a.nww = Wd / 8; a.H = H; a.W = Wd;
-        a.shift = shift; a.pixel_mode = 1; a.scale = h->scale; a.wide = h->attn64;
+        a.shift = shift; a.pixel_mode = 1; a.scale = h->scale; a.wide = h->attn64; a.qsplit = h->attn_qs;
         long nw = long(a.nwh) * a.nww;
         Span sp(h, "attention", 16384.0 * t * nw, 4.0 * 64.0 * nw * 4 * t);
         const char* why = nullptr;
@@ -886,6 +887,8 @@ static int create_handle(const char* path, const scunet_hip_arch_info* arch, scu
     h->wino3_all = std::getenv("SCUNET_HIP_WINO3") != nullptr;
     // A/B switch: the attention kernel's 64-bit-offset form at every size.
     h->attn64 = std::getenv("SCUNET_HIP_ATTN64") != nullptr;
+    // A/B switch: the attention kernel with 1 or 2 query parts per (window, head).
+    if (const char* q = std::getenv("SCUNET_HIP_ATTN_QS")) h->attn_qs = std::atoi(q) == 2 ? 2 : 1;
     h->gemm2 = std::getenv("SCUNET_HIP_GEMM2") != nullptr;
     h->gemm1x1 = std::getenv("SCUNET_HIP_GEMM1X1") != nullptr;
     h->separate_mlp = std::getenv("SCUNET_HIP_SEPARATE_MLP") != nullptr;
@@ -1331,7 +1334,7 @@ int scunet_hip_attention_kernel_probe(scunet_hip* h, size_t hh, size_t ww, size_
         AttnArgs a;
         a.qkv = dq; a.ldq = long(3 * c); a.out = y; a.ldo = long(c); a.tab = dt; a.C = int(c); a.heads = int(heads);
         a.nwh = int(hh / 8); a.nww = int(ww / 8); a.H = int(hh); a.W = int(ww); a.shift = int(shift);
-        a.pixel_mode = 0; a.scale = std::pow(float(hd), -0.5f); a.wide = h->attn64;
+        a.pixel_mode = 0; a.scale = std::pow(float(hd), -0.5f); a.wide = h->attn64; a.qsplit = h->attn_qs;
         const char* why = nullptr;
         if (!attention(a, h->stream, &why)) return fail(h, why);
         if (!launched(h, "attention probe")) return false;
@@ -1401,7 +1404,7 @@ int scunet_hip_attention_probe(scunet_hip* h, const char* prefix, size_t hh, siz
         AttnArgs a;
         a.qkv = qkv; a.ldq = 3 * t; a.out = att; a.ldo = t; a.tab = h->atab[prefix]; a.C = t;
         a.heads = t / h->wt.head_dim; a.nwh = int(hh / 8); a.nww = int(ww / 8); a.H = int(hh); a.W = int(ww);
-        a.shift = int(shift); a.pixel_mode = 1; a.scale = h->scale; a.wide = h->attn64;
+        a.shift = int(shift); a.pixel_mode = 1; a.scale = h->scale; a.wide = h->attn64; a.qsplit = h->attn_qs;
         const char* why = nullptr;
         if (!attention(a, h->stream, &why)) return fail(h, why);
         g = GemmArgs{};
@@ -1425,7 +1428,7 @@ int scunet_hip_bench_attn(scunet_hip* h, const float* qkv, const float* rp, floa
         AttnArgs a;
         a.qkv = qkv; a.ldq = long(3 * c); a.out = out; a.ldo = long(c); a.tab = dt; a.C = int(c);
         a.heads = int(heads); a.nwh = int(nwh); a.nww = int(nww); a.H = int(nwh * 8); a.W = int(nww * 8);
-        a.shift = int(shift); a.pixel_mode = 0; a.scale = h->scale; a.wide = h->attn64;
+        a.shift = int(shift); a.pixel_mode = 0; a.scale = h->scale; a.wide = h->attn64; a.qsplit = h->attn_qs;
         const char* why = nullptr;
         for (int i = 0; i < 3; ++i)
             if (!attention(a, h->stream, &why)) return fail(h, why);

@@ -168,6 +168,7 @@ struct AttnArgs {
     int pixel_mode = 1;            // 1: rows are pixels y*W+x; 0: rows are window*64+token
     float scale = 0.f;
     int wide = 0;                  // 1: 64-bit element offsets even where 32-bit ones would do
+    int qsplit = 0;                // query parts per (window, head): 0 automatic, 1 or 2
 };
 // 8x8 windows, head_dim 32, at most 8 heads.
 bool attention(const AttnArgs& a, hipStream_t s, const char** why);

@@ -2511,7 +2511,7 @@ void winograd_filter_slices(const float* u, int cout, int cin, float* u8) {
 // loads, 64 contiguous bytes per key), so the only LDS is the 7.2 KB of tables and the
 // kernel fits in 128 VGPRs: four waves per SIMD, 4 096 (window, head) units in flight.
 // ---------------------------------------------------------------------------
-template <bool WIDE>
+template <bool WIDE, int QS>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4))) void k_attention(AttnArgs a, long units) {
     // Element offsets: 32-bit (WIDE = false) unless the qkv plane reaches 2^32 elements.
     using U = typename std::conditional<WIDE, unsigned long, unsigned>::type;
@@ -2522,9 +2522,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
     const long u = long(blockIdx.x) * 4 + wave;
     if (u >= units) return;                      // whole wave exits together
     const int li = lane & 15, lg = lane >> 4;
-    // (window, head) and window indices fit 32 bits (the launch grid is 32-bit).
-    const unsigned wi = unsigned(u) / unsigned(a.heads);
-    const int h = int(unsigned(u) - wi * unsigned(a.heads));
+    // A unit is (window, head, query part): QS parts of NQ = 4 / QS query tiles each. Unit
+    // and window indices fit 32 bits (the launch grid is 32-bit).
+    constexpr int NQ = 4 / QS;
+    const unsigned wh_u = unsigned(u) / unsigned(QS);
+    const int part = int(unsigned(u) - wh_u * unsigned(QS));
+    const unsigned wi = wh_u / unsigned(a.heads);
+    const int h = int(wh_u - wi * unsigned(a.heads));
     const int wh = int(wi / unsigned(a.nww)), ww = int(wi - unsigned(wh) * unsigned(a.nww));
     const int hoff = h * 32;
 
@@ -2534,7 +2538,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
     // instruction). In pixel mode token (ty, tx) of window (wh, ww) is pixel
     // ((8wh + ty + shift) mod H, (8ww + tx + shift) mod W) (cpu.rs:648-652's cyclic shift
     // folded into the addressing).
-    U off[4], vy[4], vx[4];
+    U off[4], offq[NQ], vy[4], vx[4];
     if (a.pixel_mode) {
         auto wy = [&](int ty) { int y = wh * 8 + ty + a.shift; return U(y >= a.H ? y - a.H : y); };
         auto wx = [&](int tx) { int x = ww * 8 + tx + a.shift; return U(x >= a.W ? x - a.W : x); };
@@ -2542,12 +2546,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
 #pragma unroll
         for (int m = 0; m < 4; ++m) off[m] = (wy(2 * m + (li >> 3)) * U(a.W) + xq) * U(a.ldq);
 #pragma unroll
+        for (int j = 0; j < NQ; ++j) offq[j] = (wy(2 * (part * NQ + j) + (li >> 3)) * U(a.W) + xq) * U(a.ldq);
+#pragma unroll
         for (int kt = 0; kt < 4; ++kt) vy[kt] = wy(2 * kt + (lg >> 1)) * U(a.W);
 #pragma unroll
         for (int r = 0; r < 4; ++r) vx[r] = wx(4 * (lg & 1) + r);
     } else {
 #pragma unroll
         for (int m = 0; m < 4; ++m) off[m] = (U(wi) * 64u + 16u * m + li) * U(a.ldq);
+#pragma unroll
+        for (int j = 0; j < NQ; ++j) offq[j] = (U(wi) * 64u + 16u * (part * NQ + j) + li) * U(a.ldq);
 #pragma unroll
         for (int kt = 0; kt < 4; ++kt) vy[kt] = U(wi) * 64u + 16u * kt + 4u * lg;
 #pragma unroll
@@ -2571,14 +2579,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
     // All of the window-head's operands are requested before the first product.
     // kf / qf: token 16m + li, dims 16G + 4lg .. +3. vv: the A operand of O^T = V^T P^T,
     // dim 16nd + li against keys 16kt + 4lg + r.
-    f4 kf[4][2], qf[4][2], vv[4][2];
+    f4 kf[4][2], qf[NQ][2], vv[4][2];
 #pragma unroll
     for (int m = 0; m < 4; ++m)
 #pragma unroll
-        for (int G = 0; G < 2; ++G) {
-            kf[m][G] = ld4(k_base + off[m] + G * 16 + lg * 4);
-            qf[m][G] = ld4(q_base + off[m] + G * 16 + lg * 4);
-        }
+        for (int G = 0; G < 2; ++G) kf[m][G] = ld4(k_base + off[m] + G * 16 + lg * 4);
+#pragma unroll
+    for (int j = 0; j < NQ; ++j)
+#pragma unroll
+        for (int G = 0; G < 2; ++G) qf[j][G] = ld4(q_base + offq[j] + G * 16 + lg * 4);
 #pragma unroll
     for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
@@ -2600,7 +2609,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
     const float sc = a.scale * 1.4426950408889634f;   // logits in log2 units: p = 2^(l - max)
 
 #pragma unroll
-    for (int nt = 0; nt < 4; ++nt) {
+    for (int j = 0; j < NQ; ++j) {
+        const int nt = part * NQ + j;
         f4 S[4];
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt) S[mt] = f4{0.f, 0.f, 0.f, 0.f};
@@ -2609,7 +2619,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
 #pragma unroll
             for (int s4 = 0; s4 < 4; ++s4)
 #pragma unroll
-                for (int mt = 0; mt < 4; ++mt) S[mt] = mfma4(kf[mt][G][s4], qf[nt][G][s4], S[mt]);
+                for (int mt = 0; mt < 4; ++mt) S[mt] = mfma4(kf[mt][G][s4], qf[j][G][s4], S[mt]);
         // Logits for query 16nt + li against keys 16mt + 4lg + r.
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt)
@@ -2665,11 +2675,21 @@ bool attention(const AttnArgs& a, hipStream_t s, const char** why) {
     const bool wide = a.wide || rows * double(a.ldq) >= 4294967296.0 || rows * double(a.ldo) >= 4294967296.0;
     if (a.shift != 0 && a.shift != 4) { *why = "attention: the shifted-window mask assumes shift 4"; return false; }
     if (a.heads > 8) { *why = "attention: at most 8 heads"; return false; }
-    long units = long(a.nwh) * a.nww * a.heads;
-    if (units == 0) return true;
+    const long wheads = long(a.nwh) * a.nww * a.heads;
+    if (wheads == 0) return true;
+    // Two query parts per (window, head) when the (window, head) units alone would not give
+    // the chip two rounds of waves, so that loads, products and stores of different waves
+    // overlap (the key and value rows are then read by both parts, from L2 the second time).
+    const int qs = a.qsplit ? a.qsplit : (wheads <= 4096 ? 2 : 1);
+    const long units = wheads * qs;
     dim3 grid(unsigned((units + 3) / 4));
-    if (wide) hipLaunchKernelGGL(k_attention<true>, grid, dim3(256), 0, s, a, units);
-    else hipLaunchKernelGGL(k_attention<false>, grid, dim3(256), 0, s, a, units);
+    if (qs == 2) {
+        if (wide) hipLaunchKernelGGL((k_attention<true, 2>), grid, dim3(256), 0, s, a, units);
+        else hipLaunchKernelGGL((k_attention<false, 2>), grid, dim3(256), 0, s, a, units);
+    } else {
+        if (wide) hipLaunchKernelGGL((k_attention<true, 1>), grid, dim3(256), 0, s, a, units);
+        else hipLaunchKernelGGL((k_attention<false, 1>), grid, dim3(256), 0, s, a, units);
+    }
     return true;
 }
 
