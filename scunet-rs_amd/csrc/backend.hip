@@ -111,6 +111,13 @@ struct scunet_hip {
     size_t h16bytes = 0;
     std::map<std::string, const half_t*> hw;
     std::map<const float*, const half_t*> hw_of;   // fp32 device pointer -> its fp16 copy
+    // The split-operand fp32 products (x6): three bf16 part planes per matrix weight, built
+    // at create; x6 = false sends every fp32 product to the fp32 matrix cores instead.
+    bool x6 = false;
+    bf16_t* x6blob = nullptr;
+    size_t x6bytes = 0;
+    std::map<std::string, const bf16_t*> xw;
+    std::map<const float*, const bf16_t*> xw_of;
     std::string tag;                     // appended to profiler class names ("@L0".."@L3")
     std::vector<ProfRec> recs;
     std::vector<hipEvent_t> ev_pool;
@@ -124,6 +131,7 @@ struct scunet_hip {
             if (kv.second.first) hipFree(kv.second.first);
         if (wblob) hipFree(wblob);
         if (h16blob) hipFree(h16blob);
+        if (x6blob) hipFree(x6blob);
         for (auto e : ev_pool) hipEventDestroy(e);
         if (stream) hipStreamDestroy(stream);
     }
@@ -228,6 +236,14 @@ const half_t* W16(scunet_hip* h, const std::string& name) {
     return it == h->hw.end() ? nullptr : it->second;
 }
 
+// The split planes of weight `name` when the handle computes fp32 products in split form,
+// else null (which selects a kernel's fp32-MFMA path).
+const bf16_t* WX(scunet_hip* h, const std::string& name) {
+    if (h->h16 || !h->x6) return nullptr;
+    auto it = h->xw.find(name);
+    return it == h->xw.end() ? nullptr : it->second;
+}
+
 // Upload every tensor once (cuda.rs:466-472 uploads lazily; here all at create), in the
 // layout its kernel reads:
 //   3x3 conv_block weights [co][ci][3][3] -> [tap][co][ci], and as Winograd filters [16][co][ci]
@@ -309,13 +325,12 @@ bool upload_weights(scunet_hip* h) {
     return true;
 }
 
-// The fp16 mode's weight copies: every matrix weight whose reduction width K is a multiple
-// of 32, as [rows][K] in the layout the fp32 kernels read (after the repacking above),
-// converted and k-permuted on the device.
-bool build_h16_weights(scunet_hip* h) {
-    if (h->h16blob) return true;
+// The matrix weights the 16-bit layouts cover: every weight whose reduction width K is a
+// multiple of 32, as [rows][K] in the layout the fp32 kernels read (after the repacking above).
+struct MatItem { const float* src; long rows; int K; std::string name; };
+std::vector<MatItem> matrix_weights(scunet_hip* h) {
     const Weights& wt = h->wt;
-    struct Item { const float* src; long rows; int K; std::string name; };
+    using Item = MatItem;
     std::vector<Item> items;
     for (auto& kv : wt.all()) {
         const std::string& n = kv.first;
@@ -339,6 +354,13 @@ bool build_h16_weights(scunet_hip* h) {
         if (!src) continue;
         items.push_back({src, rows, K, n});
     }
+    return items;
+}
+
+// The fp16 mode's weight copies, converted and k-permuted on the device.
+bool build_h16_weights(scunet_hip* h) {
+    if (h->h16blob) return true;
+    const std::vector<MatItem> items = matrix_weights(h);
     size_t total = 0;
     for (auto& it : items) total += (size_t(it.rows) * it.K * 2 + 255) / 256 * 256;
     void* p = nullptr;
@@ -356,6 +378,27 @@ bool build_h16_weights(scunet_hip* h) {
     return ck(h, hipStreamSynchronize(h->stream), "fp16 weights");
 }
 
+// The split weight planes (three bf16 planes per matrix weight, k-permuted like the fp16 copy).
+bool build_x6_weights(scunet_hip* h) {
+    if (h->x6blob) return true;
+    const std::vector<MatItem> items = matrix_weights(h);
+    size_t total = 0;
+    for (auto& it : items) total += (size_t(it.rows) * it.K * 6 + 255) / 256 * 256;
+    void* p = nullptr;
+    if (!ck(h, hipMalloc(&p, std::max<size_t>(total, 256)), "split weights: hipMalloc")) return false;
+    h->x6blob = static_cast<bf16_t*>(p);
+    h->x6bytes = total;
+    char* at = static_cast<char*>(p);
+    for (auto& it : items) {
+        x6_permute(it.src, reinterpret_cast<bf16_t*>(at), it.rows, it.K, h->stream);
+        if (!launched(h, "split weights")) return false;
+        h->xw[it.name] = reinterpret_cast<const bf16_t*>(at);
+        h->xw_of[it.src] = reinterpret_cast<const bf16_t*>(at);
+        at += (size_t(it.rows) * it.K * 6 + 255) / 256 * 256;
+    }
+    return ck(h, hipStreamSynchronize(h->stream), "split weights");
+}
+
 // Algorithmic FLOP / bytes for the profiler (fp32, 2 FLOP per multiply-add; bytes =
 // inputs read once + outputs written once).
 double gemm_flop(long M, int N, int K) { return 2.0 * double(M) * N * K; }
@@ -370,6 +413,9 @@ bool run_gemm(scunet_hip* h, const char* cls, const GemmArgs& g, GemmA a, GemmE 
     if (h->h16 && !h->gemm2) {
         auto it = h->hw_of.find(g.W);
         if (it != h->hw_of.end()) gg.W16 = it->second;
+    } else if (h->x6 && !h->gemm2) {
+        auto it = h->xw_of.find(g.W);
+        if (it != h->xw_of.end()) gg.WX = it->second;
     }
     if (!gemm(gg, a, e, h->stream, &why)) return fail(h, std::string(cls) + ": " + why);
     return launched(h, cls);
@@ -457,6 +503,24 @@ bool run_pconv(scunet_hip* h, const PconvArgs& a, PconvMode mode) {
     const char* why = nullptr;
     PconvArgs aa = a;
     aa.h16 = h->h16;
+    if (!h->h16 && h->x6) {
+        auto find = [&](const float* w) -> const bf16_t* {
+            auto it = h->xw_of.find(w);
+            return it == h->xw_of.end() ? nullptr : it->second;
+        };
+        aa.x = find(a.W);
+        aa.x1 = a.W1 ? find(a.W1) : nullptr;
+        if (mode == PC_CHAIN && a.c == 128 && aa.x && aa.x1) {
+            // The split chained form does not fit the LDS at 128 channels: the block output
+            // goes through HBM between the two products.
+            PconvArgs second = aa;
+            second.A = a.C; second.W = a.W1; second.b = a.b1; second.C = a.C2; second.x = aa.x1;
+            second.R = nullptr; second.W1 = nullptr; second.x1 = nullptr; second.C2 = nullptr;
+            if (!pconv(aa, PC_RESID, h->stream, &why) || !pconv(second, PC_STORE, h->stream, &why))
+                return fail(h, why);
+            return launched(h, "conv1x1");
+        }
+    }
     if (!pconv(aa, mode, h->stream, &why)) return fail(h, why);
     return launched(h, "conv1x1");
 }
@@ -509,11 +573,13 @@ bool block(scunet_hip* h, const std::string& p, float* x, int H, int Wd, int shi
         m.t = t; m.nwh = H / 8; m.nww = Wd / 8; m.H = H; m.W = Wd; m.shift = shift; m.scale = h->scale;
         m.nimg = nimg;
         m.hqkv = W16(h, tp + ".msa.embedding_layer.weight"); m.hp = W16(h, tp + ".msa.linear.weight");
+        m.xqkv = WX(h, tp + ".msa.embedding_layer.weight"); m.xp = WX(h, tp + ".msa.linear.weight");
         if (mlp_in_msa) {
             m.ln2_g = W(h, tp + ".ln2.weight"); m.ln2_b = W(h, tp + ".ln2.bias");
             m.w0 = W(h, tp + ".mlp.0.weight"); m.b0 = W(h, tp + ".mlp.0.bias");
             m.w2 = W(h, tp + ".mlp.2.weight"); m.b2 = W(h, tp + ".mlp.2.bias");
             m.h0 = W16(h, tp + ".mlp.0.weight"); m.h2 = W16(h, tp + ".mlp.2.weight");
+            m.x0 = WX(h, tp + ".mlp.0.weight"); m.x2 = WX(h, tp + ".mlp.2.weight");
             m.gelu = W(h, "@gelu");
         }
         const double nw = double(m.nwh) * m.nww * nimg;
@@ -532,6 +598,7 @@ bool block(scunet_hip* h, const std::string& p, float* x, int H, int Wd, int shi
         m.w0 = W(h, tp + ".mlp.0.weight"); m.b0 = W(h, tp + ".mlp.0.bias");
         m.w2 = W(h, tp + ".mlp.2.weight"); m.b2 = W(h, tp + ".mlp.2.bias"); m.M = P; m.t = t;
         m.h0 = W16(h, tp + ".mlp.0.weight"); m.h2 = W16(h, tp + ".mlp.2.weight");
+        m.x0 = WX(h, tp + ".mlp.0.weight"); m.x2 = WX(h, tp + ".mlp.2.weight");
         m.gelu = W(h, "@gelu");
         Span sp(h, "mlp_fused", mlp_flop, 4.0 * (2.0 * P * t + 8.0 * t * t + 5.0 * t));
         const char* why = nullptr;
@@ -776,7 +843,7 @@ bool preflight(scunet_hip* h, size_t H, size_t W, size_t io, bool dump) {
     return fail(h, "a " + std::to_string(H) + "x" + std::to_string(W) + " forward needs " +
                        std::to_string(need.second >> 20) + " MiB more device memory (" +
                        std::to_string(need.first >> 20) + " MiB of scratch in all, plus " +
-                       std::to_string((h->wbytes + h->h16bytes) >> 20) + " MiB of weights); the device has " +
+                       std::to_string((h->wbytes + h->h16bytes + h->x6bytes) >> 20) + " MiB of weights); the device has " +
                        std::to_string(free_b >> 20) + " MiB free of " + std::to_string(total_b >> 20) + " MiB");
 }
 
@@ -895,6 +962,14 @@ static int create_handle(const char* path, const scunet_hip_arch_info* arch, scu
     if (!upload_weights(h.get())) {
         g_create_error = h->err;
         return 1;
+    }
+    // A/B switch (development): fp32 products in split form where a kernel has one.
+    if (std::getenv("SCUNET_HIP_X6") != nullptr) {
+        h->x6 = true;
+        if (!build_x6_weights(h.get())) {
+            g_create_error = h->err;
+            return 1;
+        }
     }
     if (arch) h->wt.forget_data();   // the caller's buffers are not ours beyond this call
     *out = h.release();
@@ -1082,7 +1157,7 @@ int scunet_hip_footprint(const scunet_hip* h, size_t* weight_bytes, size_t* scra
     if (!h) return -1;
     size_t s = 0;
     for (auto& kv : h->arena) s += kv.second.second;
-    if (weight_bytes) *weight_bytes = h->wbytes + h->h16bytes;
+    if (weight_bytes) *weight_bytes = h->wbytes + h->h16bytes + h->x6bytes;
     if (scratch_bytes) *scratch_bytes = s;
     return 0;
 }

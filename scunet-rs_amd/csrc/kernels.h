@@ -26,6 +26,15 @@ namespace scunet {
 using half_t = _Float16;
 void h16_permute(const float* src, half_t* dst, long rows, int K, hipStream_t s);
 
+// The split-operand fp32 products (the default fp32 mode where a kernel has them): an fp32
+// weight is kept as three bf16 parts h + m + l equal to it exactly, in three planes of the
+// fp16 copy's layout and k permutation, plane p at element offset p * rows * K. Each product
+// is formed from the six part products larger than 2^-25 |ab| on the bf16 matrix cores with
+// fp32 accumulation (the kernels split their activation operand the same way in registers).
+// Non-null x* / WX pointers in the argument structs below select a kernel's split path.
+using bf16_t = __bf16;
+void x6_permute(const float* src, bf16_t* dst, long rows, int K, hipStream_t s);
+
 // A-operand loaders of the GEMM.
 enum GemmA {
     A_ROWS = 0,   // A[m][k] = A[m*lda + k]
@@ -64,6 +73,9 @@ struct GemmArgs {
     // fp16 mode: W k-permuted. Used by the persistent walker for N % 64 == 0, K % 32 == 0 and
     // the row, patch and skip-sum operands; other shapes keep fp32 products.
     const half_t* W16 = nullptr;
+    // Split-operand fp32 products: W as three k-permuted bf16 planes (N * K elements apart),
+    // same shape conditions as W16.
+    const bf16_t* WX = nullptr;
 };
 
 // Returns false (and a reason) if no tile configuration fits the shape.
@@ -89,6 +101,10 @@ struct PconvArgs {
     long M = 0;
     int c = 0;
     int h16 = 0;                   // fp16 MFMA operands (fp32 accumulation)
+    // Split-operand products: W (and W1) as three bf16 planes (c * c elements apart). The
+    // chained form at c = 128 has no split configuration (its six planes exceed the LDS).
+    const bf16_t* x = nullptr;
+    const bf16_t* x1 = nullptr;
 };
 // False (and a reason) for channel counts without a resident-weight configuration.
 bool pconv_supported(int c);
@@ -108,6 +124,8 @@ struct MlpArgs {
     const float* b2 = nullptr;     // [t]
     const half_t* h0 = nullptr;    // fp16 mode: W0, W2 k-permuted
     const half_t* h2 = nullptr;
+    const bf16_t* x0 = nullptr;    // split products (t = 128, 256): W0, W2 as three planes each
+    const bf16_t* x2 = nullptr;
     const float* gelu = nullptr;   // the GELU table (build_gelu_table), GELU_TABLE floats
     long M = 0;
     int t = 0;
@@ -199,6 +217,12 @@ struct MsaArgs {
     const half_t* hp = nullptr;
     const half_t* h0 = nullptr;
     const half_t* h2 = nullptr;
+    // Split-operand products: the same weights as three bf16 planes each (xqkv, xp always;
+    // x0, x2 with the MLP option).
+    const bf16_t* xqkv = nullptr;
+    const bf16_t* xp = nullptr;
+    const bf16_t* x0 = nullptr;
+    const bf16_t* x2 = nullptr;
     const float* gelu = nullptr;   // with the MLP option: the GELU table (build_gelu_table)
     int t = 0;
     int nwh = 0, nww = 0, H = 0, W = 0, shift = 0;   // nwh, H: one image's window rows and rows

@@ -42,6 +42,62 @@ DEVI f4 mfma16(h8 a, h8 b, f4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_f16
 DEVI h8 ldh8(const _Float16* p) { return *reinterpret_cast<const h8*>(p); }
 DEVI void sth8(_Float16* p, h8 v) { *reinterpret_cast<h8*>(p) = v; }
 
+// Split-operand fp32 products on the bf16 matrix cores (v_mfma_f32_16x16x32_bf16, the same
+// lane layout as the f16 product above). An fp32 value x is carried as three bf16 parts with
+// h + m + l == x exactly: h = rne(x), m = rne(x - h), l = x - h - m (both differences are
+// exact in fp32, and l has at most 8 significant bits). A product ab is then the sum of the
+// six part products whose size can exceed 2^-24 |ab|: hh + hm + mh + hl + lh + mm; the three
+// dropped (ml, lm, ll) are below 2^-25 |ab| together, under fp32's own rounding of one
+// product, and every part product is exact in the fp32 accumulator's input. Operands that
+// are weights are split once at upload (x6_permute); activations are split in registers.
+typedef __bf16 b8 __attribute__((ext_vector_type(8)));
+typedef short s8v __attribute__((ext_vector_type(8)));
+struct x8 {
+    b8 h, m, l;
+};
+DEVI f4 mfmab(b8 a, b8 b, f4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0); }
+// Two floats -> their rne bf16 parts packed in one register, and the exact remainders.
+DEVI unsigned split2(float& x0, float& x1) {
+    typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+    typedef float fl2 __attribute__((ext_vector_type(2)));
+    const b2 p = __builtin_convertvector(fl2{x0, x1}, b2);
+    const unsigned u = __builtin_bit_cast(unsigned, p);
+    x0 -= __builtin_bit_cast(float, u << 16);
+    x1 -= __builtin_bit_cast(float, u & 0xffff0000u);
+    return u;
+}
+DEVI unsigned pack2(float x0, float x1) {
+    typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+    typedef float fl2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(unsigned, __builtin_convertvector(fl2{x0, x1}, b2));
+}
+// The lane's 8 k values (the f4s of two adjacent k groups, as pack8) in split form.
+DEVI x8 split8(f4 lo, f4 hi) {
+    typedef unsigned u4 __attribute__((ext_vector_type(4)));
+    float v[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+    u4 H, M, L;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) H[i] = split2(v[2 * i], v[2 * i + 1]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) M[i] = split2(v[2 * i], v[2 * i + 1]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) L[i] = pack2(v[2 * i], v[2 * i + 1]);
+    return x8{__builtin_bit_cast(b8, H), __builtin_bit_cast(b8, M), __builtin_bit_cast(b8, L)};
+}
+// c += a b over the lane's 8 k values, a and b in split form (smallest terms first).
+DEVI f4 mfma6(const x8& a, const x8& b, f4 c) {
+    c = mfmab(a.l, b.h, c);
+    c = mfmab(a.h, b.l, c);
+    c = mfmab(a.m, b.m, c);
+    c = mfmab(a.m, b.h, c);
+    c = mfmab(a.h, b.m, c);
+    return mfmab(a.h, b.h, c);
+}
+DEVI b8 ldb8(const __bf16* p) { return *reinterpret_cast<const b8*>(p); }
+DEVI void stb8(__bf16* p, b8 v) { *reinterpret_cast<b8*>(p) = v; }
+// The three parts of a split weight fragment: part planes `ps` elements apart.
+DEVI x8 ldx8(const __bf16* p, long ps) { return x8{ldb8(p), ldb8(p + ps), ldb8(p + 2 * ps)}; }
+
 DEVI f4 ld4(const float* p) { return *reinterpret_cast<const f4*>(p); }
 // LDS row pitches: a wave's 16-byte LDS reads are conflict-free when, within each 32-lane
 // half, the 16-byte slot indices are distinct mod 32. The MFMA operand reads here have
@@ -466,19 +522,22 @@ __global__ __launch_bounds__(256) void k_gemm2(GemmArgs g) {
 // double-buffered in LDS; the epilogue uses registers only). Tile t = 8 j + xcd: the
 // N-blocks of one M-tile are consecutive j on one XCD and share its L2.
 // ---------------------------------------------------------------------------
-template <int MT, int BN, int KC, int AM, int EP, bool H16>
+template <int MT, int BN, int KC, int AM, int EP, bool H16, bool X6 = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_gemm3(GemmArgs g, long tiles) {
     // fp16 mode: a K slice is one 32-wide k block of the k-permuted weights, staged as halves
-    // with rows of 48 (2 mod 4 sixteen-byte slots: conflict-free 128-bit reads).
+    // with rows of 48 (2 mod 4 sixteen-byte slots: conflict-free 128-bit reads). The split
+    // products (X6) stage the three bf16 part planes of the slice the same way.
     static_assert(!H16 || KC == 32, "fp16 slices are one k block");
+    static_assert(!X6 || H16, "split products use the 16-bit layout");
     constexpr int NT = BN / 16, KG = KC / 16, LDB = H16 ? 48 : KC + 8;
     constexpr int EV = H16 ? 8 : 4;               // elements per 16-byte chunk
+    constexpr int NP = X6 ? 3 : 1;                // weight planes
     constexpr int BV = BN * KC / EV / 256;
     static_assert(BN * KC / EV % 256 == 0, "weight slice must split evenly over 256 threads");
     // The residual is read ahead when its registers fit (up to 8 float4 per lane).
     constexpr bool RPRE = EP == E_RESID && MT * NT <= 8;
-    using ET = std::conditional_t<H16, _Float16, float>;
-    __shared__ __align__(16) ET Bs[2 * BN * LDB];
+    using ET = std::conditional_t<X6, __bf16, std::conditional_t<H16, _Float16, float>>;
+    __shared__ __align__(16) ET Bs[2 * NP * BN * LDB];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int li = lane & 15, lg = lane >> 4;
@@ -505,23 +564,33 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         }
         return ld4(g.A + row * g.lda + k);
     };
-    f4 bpre[BV];
+    f4 bpre[NP * BV];
+    const long wps = long(g.N) * g.K;   // X6: part plane stride
     auto bload = [&](int n0, int k0) {
 #pragma unroll
         for (int i = 0; i < BV; ++i) {
             const int f = tid + i * 256;
             const int row = f / (KC / EV), c = f % (KC / EV);
-            if constexpr (H16) bpre[i] = ld4(reinterpret_cast<const float*>(g.W16 + long(n0 + row) * g.K + k0 + c * 8));
-            else bpre[i] = ld4(g.W + long(n0 + row) * g.K + k0 + c * 4);
+            if constexpr (X6) {
+#pragma unroll
+                for (int p = 0; p < NP; ++p)
+                    bpre[p * BV + i] = ld4(reinterpret_cast<const float*>(g.WX + p * wps + long(n0 + row) * g.K + k0 + c * 8));
+            } else if constexpr (H16) {
+                bpre[i] = ld4(reinterpret_cast<const float*>(g.W16 + long(n0 + row) * g.K + k0 + c * 8));
+            } else {
+                bpre[i] = ld4(g.W + long(n0 + row) * g.K + k0 + c * 4);
+            }
         }
     };
     auto bstore = [&](int b) {
 #pragma unroll
-        for (int i = 0; i < BV; ++i) {
-            const int f = tid + i * 256;
-            const int row = f / (KC / EV), c = f % (KC / EV);
-            st4(reinterpret_cast<float*>(&Bs[b * BN * LDB + row * LDB + c * EV]), bpre[i]);
-        }
+        for (int p = 0; p < NP; ++p)
+#pragma unroll
+            for (int i = 0; i < BV; ++i) {
+                const int f = tid + i * 256;
+                const int row = f / (KC / EV), c = f % (KC / EV);
+                st4(reinterpret_cast<float*>(&Bs[(b * NP + p) * BN * LDB + row * LDB + c * EV]), bpre[p * BV + i]);
+            }
     };
     f4 acur[MT][KG], anext[MT][KG];
     auto aload = [&](long m0, int k0, f4 (&dst)[MT][KG]) {
@@ -573,8 +642,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                     }
                 }
             }
-            const ET* B = Bs + kb * BN * LDB;
-            if constexpr (H16) {
+            const ET* B = Bs + kb * NP * BN * LDB;
+            if constexpr (X6) {
+                x8 ap[MT];
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) ap[mt] = split8(acur[mt][0], acur[mt][1]);
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt) {
+                    const x8 bx = ldx8(B + (nt * 16 + li) * LDB + lg * 8, BN * LDB);
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt) acc[mt][nt] = mfma6(bx, ap[mt], acc[mt][nt]);
+                }
+            } else if constexpr (H16) {
                 h8 ap[MT];
 #pragma unroll
                 for (int mt = 0; mt < MT; ++mt) ap[mt] = pack8(acur[mt][0], acur[mt][1]);
@@ -666,26 +745,26 @@ static bool query_occ(K kernel, int threads, std::atomic<int>& cus_c, std::atomi
     return true;
 }
 
-template <int MT, int BN, int KC, int AM, int EP, bool H16>
+template <int MT, int BN, int KC, int AM, int EP, bool H16, bool X6>
 static void launch_gemm3_k(const GemmArgs& g, hipStream_t s) {
     static std::atomic<int> cus_c{0}, pc_c{0};
     Occ oc;
-    if (!query_occ(k_gemm3<MT, BN, KC, AM, EP, H16>, 256, cus_c, pc_c, &oc)) oc = Occ{256, 1};
+    if (!query_occ(k_gemm3<MT, BN, KC, AM, EP, H16, X6>, 256, cus_c, pc_c, &oc)) oc = Occ{256, 1};
     const int cus = oc.cus, per_cu = oc.per_cu;
     const long mtiles = (g.M + 64 * MT - 1) / (64 * MT);
     const long tiles = ((mtiles + 7) / 8) * 8 * (g.N / BN);
     dim3 grid{unsigned(std::min<long>(tiles, long(cus) * per_cu)), 1u, 1u}, block{256u, 1u, 1u};
-    hipLaunchKernelGGL((k_gemm3<MT, BN, KC, AM, EP, H16>), grid, block, 0, s, g, tiles);
+    hipLaunchKernelGGL((k_gemm3<MT, BN, KC, AM, EP, H16, X6>), grid, block, 0, s, g, tiles);
 }
 
-template <int MT, int BN, int KC, int AM, bool H16 = false>
+template <int MT, int BN, int KC, int AM, bool H16 = false, bool X6 = false>
 static void launch_gemm3_e(const GemmArgs& g, GemmE e, hipStream_t s) {
     switch (e) {
-        case E_STORE: launch_gemm3_k<MT, BN, KC, AM, E_STORE, H16>(g, s); break;
-        case E_DUAL: launch_gemm3_k<MT, BN, KC, AM, E_DUAL, H16>(g, s); break;
-        case E_GELU: launch_gemm3_k<MT, BN, KC, AM, E_GELU, H16>(g, s); break;
-        case E_RESID: launch_gemm3_k<MT, BN, KC, AM, E_RESID, H16>(g, s); break;
-        case E_D2S: launch_gemm3_k<MT, BN, KC, AM, E_D2S, H16>(g, s); break;
+        case E_STORE: launch_gemm3_k<MT, BN, KC, AM, E_STORE, H16, X6>(g, s); break;
+        case E_DUAL: launch_gemm3_k<MT, BN, KC, AM, E_DUAL, H16, X6>(g, s); break;
+        case E_GELU: launch_gemm3_k<MT, BN, KC, AM, E_GELU, H16, X6>(g, s); break;
+        case E_RESID: launch_gemm3_k<MT, BN, KC, AM, E_RESID, H16, X6>(g, s); break;
+        case E_D2S: launch_gemm3_k<MT, BN, KC, AM, E_D2S, H16, X6>(g, s); break;
     }
 }
 
@@ -708,9 +787,27 @@ static void launch_gemm3_h16(const GemmArgs& g, GemmA a, GemmE e, hipStream_t s)
     }
 }
 
+template <int MT, int BN>
+static void launch_gemm3_x6(const GemmArgs& g, GemmA a, GemmE e, hipStream_t s) {
+    switch (a) {
+        case A_ROWS: launch_gemm3_e<MT, BN, 32, A_ROWS, true, true>(g, e, s); break;
+        case A_S2D: launch_gemm3_e<MT, BN, 32, A_S2D, true, true>(g, e, s); break;
+        case A_ADD2: launch_gemm3_e<MT, BN, 32, A_ADD2, true, true>(g, e, s); break;
+        default: break;
+    }
+}
+
 static bool launch_gemm3(const GemmArgs& g, GemmA a, GemmE e, hipStream_t s) {
     // k_gemm3 decodes tile indices in 32 bits (at most 2^31 tiles of 16 rows or more).
     if (g.M / 16 >= (1L << 31)) return false;
+    if (g.WX && a != A_LN && g.K % 32 == 0 && g.N % 64 == 0) {
+        // Split products: at least two 16-row tiles per wave, so the three weight planes a
+        // wave reads from LDS per k block feed twice as many products (one tile per wave
+        // would need the whole LDS bandwidth).
+        if (g.N % 128 == 0) launch_gemm3_x6<2, 128>(g, a, e, s);
+        else launch_gemm3_x6<2, 64>(g, a, e, s);
+        return true;
+    }
     if (g.W16 && a != A_LN && g.K % 32 == 0 && g.N % 64 == 0) {
         // The level-0 down-conv (N = 128) reads its patches once with a 128-wide N block:
         // 382 -> 268 us per launch; the other shapes measured best as below.
@@ -848,20 +945,31 @@ bool gemm(const GemmArgs& g, GemmA a, GemmE e, hipStream_t s, const char** why) 
 // M rows), which leaves each lane holding 4 consecutive output channels of one pixel:
 // a float4 store, and, when chaining, exactly the pixel operand of the next product.
 // ---------------------------------------------------------------------------
-template <int C, int MT, int NW, int MODE, bool RPRE, bool H16>
+template <int C, int MT, int NW, int MODE, bool RPRE, bool H16, bool X6 = false>
 __global__ __launch_bounds__(NW * 64) void k_pconv(PconvArgs a) {
+    static_assert(!X6 || H16, "split products use the 16-bit layout");
     constexpr int NT = C / 16, KG = C / 16;
-    // fp32 rows: pitch C + 8 floats; fp16 rows: pitch C + 16 halves. Either way the pitch
+    // fp32 rows: pitch C + 8 floats; 16-bit rows: pitch C + 16 halves. Either way the pitch
     // is 2 mod 4 sixteen-byte slots, so the 16 rows x 2 slots a 32-lane half reads are
-    // distinct mod 32: conflict-free 128-bit reads.
+    // distinct mod 32: conflict-free 128-bit reads. Split weights: three such planes.
     constexpr int LDW = H16 ? C + 16 : C + 8;
     constexpr int NMAT = MODE == PC_CHAIN ? 2 : 1;
-    using WT = std::conditional_t<H16, _Float16, float>;
-    __shared__ __align__(16) WT Ws[NMAT * C * LDW];
+    constexpr int NP = X6 ? 3 : 1;
+    constexpr int MSTR = NP * C * LDW;   // one matrix (all its planes)
+    using WT = std::conditional_t<X6, __bf16, std::conditional_t<H16, _Float16, float>>;
+    __shared__ __align__(16) WT Ws[NMAT * MSTR];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int li = lane & 15, lg = lane >> 4;
 
-    if constexpr (H16) {
+    if constexpr (X6) {
+        // The pre-split planes (already in the k order of the products), 16 bytes at a time.
+        for (int f = tid; f < NMAT * NP * C * C / 8; f += NW * 64) {
+            const int m = f / (NP * C * C / 8), p = (f / (C * C / 8)) % NP;
+            const int r = (f / (C / 8)) % C, q = f % (C / 8);
+            const __bf16* src = (m ? a.x1 : a.x) + long(p) * C * C + long(r) * C + q * 8;
+            stb8(&Ws[m * MSTR + p * C * LDW + r * LDW + q * 8], ldb8(src));
+        }
+    } else if constexpr (H16) {
         // Halves in the order the f16 product reads them: slot q = 4 kk + lg of row r holds
         // W[r][32 kk + 4 lg + 0..3] and W[r][32 kk + 16 + 4 lg + 0..3].
         for (int f = tid; f < NMAT * C * C / 8; f += NW * 64) {
@@ -896,7 +1004,20 @@ __global__ __launch_bounds__(NW * 64) void k_pconv(PconvArgs a) {
         for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
             for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = f4{0.f, 0.f, 0.f, 0.f};
-        if constexpr (H16) {
+        if constexpr (X6) {
+#pragma unroll
+            for (int kk = 0; kk < KG / 2; ++kk) {
+                x8 xv[MT];
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) xv[mt] = split8(x[mt][2 * kk], x[mt][2 * kk + 1]);
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt) {
+                    const x8 w = ldx8(Wm + (nt * 16 + li) * LDW + kk * 32 + lg * 8, C * LDW);
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt) acc[mt][nt] = mfma6(w, xv[mt], acc[mt][nt]);
+                }
+            }
+        } else if constexpr (H16) {
 #pragma unroll
             for (int kk = 0; kk < KG / 2; ++kk) {
                 h8 w[NT];
@@ -968,7 +1089,7 @@ __global__ __launch_bounds__(NW * 64) void k_pconv(PconvArgs a) {
         }
         if constexpr (MODE == PC_CHAIN) {
             f4 acc2[MT][NT];
-            product(Wg + C * LDW, acc, acc2);
+            product(Wg + MSTR, acc, acc2);
 #pragma unroll
             for (int nt = 0; nt < NT; ++nt) {
                 const f4 bv = ld4(a.b1 + nt * 16 + lg * 4);
@@ -996,16 +1117,16 @@ __global__ __launch_bounds__(NW * 64) void k_pconv(PconvArgs a) {
     }
 }
 
-template <int C, int MT, int NW, int MODE, bool RPRE, bool H16 = false>
+template <int C, int MT, int NW, int MODE, bool RPRE, bool H16 = false, bool X6 = false>
 static bool launch_pconv(const PconvArgs& a, hipStream_t s) {
     static std::atomic<int> cus_c{0}, pc_c{0};
     Occ oc;
-    if (!query_occ(k_pconv<C, MT, NW, MODE, RPRE, H16>, NW * 64, cus_c, pc_c, &oc)) return false;
+    if (!query_occ(k_pconv<C, MT, NW, MODE, RPRE, H16, X6>, NW * 64, cus_c, pc_c, &oc)) return false;
     const int cus = oc.cus, per_cu = oc.per_cu;
     const long groups = (a.M + 16 * MT - 1) / (16 * MT);
     const long waves = std::min<long>(groups, long(cus) * per_cu * NW);
     dim3 grid{unsigned((waves + NW - 1) / NW), 1u, 1u}, block{unsigned(NW * 64), 1u, 1u};
-    hipLaunchKernelGGL((k_pconv<C, MT, NW, MODE, RPRE, H16>), grid, block, 0, s, a);
+    hipLaunchKernelGGL((k_pconv<C, MT, NW, MODE, RPRE, H16, X6>), grid, block, 0, s, a);
     return true;
 }
 
@@ -1014,7 +1135,16 @@ bool pconv_supported(int c) { return c == 64 || c == 128; }
 bool pconv(const PconvArgs& a, PconvMode mode, hipStream_t s, const char** why) {
     if (a.M <= 0) return true;
     bool ok = false;
-    if (a.h16 && a.c == 64) {
+    if (a.x && a.c == 64) {
+        // Split products, one 16-row group per wave (measured at level 0 against two: the
+        // chained pair 552 -> 445 us, the 1x1 312 -> 248 us; two groups need ~270 registers).
+        if (mode == PC_STORE) ok = launch_pconv<64, 1, 4, PC_STORE, false, true, true>(a, s);
+        else if (mode == PC_RESID) ok = launch_pconv<64, 1, 4, PC_RESID, false, true, true>(a, s);
+        else ok = launch_pconv<64, 1, 4, PC_CHAIN, false, true, true>(a, s);
+    } else if (a.x && a.c == 128 && mode != PC_CHAIN) {
+        if (mode == PC_STORE) ok = launch_pconv<128, 1, 4, PC_STORE, false, true, true>(a, s);
+        else ok = launch_pconv<128, 1, 4, PC_RESID, false, true, true>(a, s);
+    } else if (a.h16 && a.c == 64) {
         if (mode == PC_STORE) ok = launch_pconv<64, 1, 4, PC_STORE, false, true>(a, s);
         else if (mode == PC_RESID) ok = launch_pconv<64, 1, 4, PC_RESID, false, true>(a, s);
         else ok = launch_pconv<64, 1, 4, PC_CHAIN, false, true>(a, s);
@@ -1048,21 +1178,26 @@ bool pconv(const PconvArgs& a, PconvMode mode, hipStream_t s, const char** why) 
 // H[row li][4 consecutive hidden units]: exactly the A operand of the second product, so
 // the hidden never goes through LDS or HBM. W0/W2 slices are double-buffered in LDS.
 // ---------------------------------------------------------------------------
-template <int T, int MT, int HC, bool H16, int NWV = 4, bool KEEP = true>
+template <int T, int MT, int HC, bool H16, int NWV = 4, bool KEEP = true, bool X6 = false, bool DB = true,
+          bool XS = true>
 __global__ __launch_bounds__(NWV * 64) void k_mlp(MlpArgs a) {
     constexpr int NTH = NWV * 64;
     constexpr int KG = T / 16, NT = T / 16, HT = HC / 16, NCH = 4 * T / HC;
-    // Slice pitches: fp32 T + 8 / HC + 8 floats; fp16 T + 16 / HC + 16 halves (2 mod 4
-    // sixteen-byte slots either way: conflict-free 128-bit operand reads).
+    // Slice pitches: fp32 T + 8 / HC + 8 floats; 16-bit T + 16 / HC + 16 halves (2 mod 4
+    // sixteen-byte slots either way: conflict-free 128-bit operand reads). Split products
+    // (X6): three planes of each slice, [W0 planes][W2 planes] in a buffer.
+    static_assert(!X6 || H16, "split products use the 16-bit layout");
     constexpr int L0 = H16 ? T + 16 : T + 8, L2 = H16 ? HC + 16 : HC + 8;
-    constexpr int BUF = HC * L0 + T * L2;
+    constexpr int NP = X6 ? 3 : 1;
+    constexpr int BUF = NP * (HC * L0 + T * L2);
     constexpr int EV = H16 ? 8 : 4;               // elements per 16-byte chunk
     constexpr int W0V = HC * T / EV;              // chunks in a W0 slice (and in a W2 slice)
-    constexpr int PV = (2 * W0V) / NTH;           // chunks per thread per slice (W0 then W2)
-    static_assert((2 * W0V) % NTH == 0 && W0V % NTH == 0, "slice must split evenly");
+    constexpr int PV = (2 * NP * W0V) / NTH;      // chunks per thread per slice (W0 then W2)
+    static_assert((2 * NP * W0V) % NTH == 0 && W0V % NTH == 0, "slice must split evenly");
     static_assert(!H16 || HC % 32 == 0, "fp16 slices are whole 32-wide k blocks");
-    using ET = std::conditional_t<H16, _Float16, float>;
-    __shared__ __align__(16) ET lds[2 * BUF];
+    using ET = std::conditional_t<X6, __bf16, std::conditional_t<H16, _Float16, float>>;
+    // DB: double-buffered slices (one barrier per slice); else one buffer, two barriers.
+    __shared__ __align__(16) ET lds[(DB ? 2 : 1) * BUF];
     __shared__ __align__(16) float gtab[GELU_TABLE];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -1112,9 +1247,16 @@ __global__ __launch_bounds__(NWV * 64) void k_mlp(MlpArgs a) {
             xa[mt][kg] = (xa[mt][kg] - mu) * rs * g + b;
         }
     }
-    // fp16 operands of the first product (k groups 2kk, 2kk + 1 packed).
-    h8 xh[H16 ? MT : 1][H16 ? KG / 2 : 1];
-    if constexpr (H16) {
+    // 16-bit operands of the first product (k groups 2kk, 2kk + 1 packed), or their split form.
+    h8 xh[H16 && !X6 ? MT : 1][H16 && !X6 ? KG / 2 : 1];
+    // XS: the normalised rows kept in split form (else split again for every slice).
+    x8 xs[X6 && XS ? MT : 1][X6 && XS ? KG / 2 : 1];
+    if constexpr (X6 && XS) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int kk = 0; kk < KG / 2; ++kk) xs[mt][kk] = split8(xa[mt][2 * kk], xa[mt][2 * kk + 1]);
+    } else if constexpr (H16) {
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -1129,7 +1271,16 @@ __global__ __launch_bounds__(NWV * 64) void k_mlp(MlpArgs a) {
 #pragma unroll
         for (int i = 0; i < PV; ++i) {
             const int f = tid + i * NTH;
-            if (f < W0V) {
+            if constexpr (X6) {
+                const int which = f / (NP * W0V), rem = f % (NP * W0V), p = rem / W0V, g = rem % W0V;
+                if (which == 0) {
+                    const int row = g / (T / 8), c = g % (T / 8);
+                    pre[i] = ld4(reinterpret_cast<const float*>(a.x0 + long(p) * 4 * T * T + long(ch * HC + row) * T + c * 8));
+                } else {
+                    const int row = g / (HC / 8), c = g % (HC / 8);
+                    pre[i] = ld4(reinterpret_cast<const float*>(a.x2 + long(p) * 4 * T * T + long(row) * (4 * T) + ch * HC + c * 8));
+                }
+            } else if (f < W0V) {
                 const int row = f / (T / EV), c = f % (T / EV);
                 pre[i] = H16 ? ld4(reinterpret_cast<const float*>(a.h0 + long(ch * HC + row) * T + c * 8))
                              : ld4(a.w0 + long(ch * HC + row) * T + c * 4);
@@ -1146,7 +1297,16 @@ __global__ __launch_bounds__(NWV * 64) void k_mlp(MlpArgs a) {
 #pragma unroll
         for (int i = 0; i < PV; ++i) {
             const int f = tid + i * NTH;
-            if (f < W0V) {
+            if constexpr (X6) {
+                const int which = f / (NP * W0V), rem = f % (NP * W0V), p = rem / W0V, g = rem % W0V;
+                if (which == 0) {
+                    const int row = g / (T / 8), c = g % (T / 8);
+                    st4(reinterpret_cast<float*>(base + p * HC * L0 + row * L0 + c * 8), pre[i]);
+                } else {
+                    const int row = g / (HC / 8), c = g % (HC / 8);
+                    st4(reinterpret_cast<float*>(base + NP * HC * L0 + p * T * L2 + row * L2 + c * 8), pre[i]);
+                }
+            } else if (f < W0V) {
                 const int row = f / (T / EV), c = f % (T / EV);
                 st4(reinterpret_cast<float*>(base + row * L0 + c * EV), pre[i]);
             } else {
@@ -1167,14 +1327,28 @@ __global__ __launch_bounds__(NWV * 64) void k_mlp(MlpArgs a) {
     lstore(0);
     __syncthreads();
     for (int ch = 0; ch < NCH; ++ch) {
-        const ET* cur = lds + (ch & 1) * BUF;
+        const ET* cur = lds + (DB ? (ch & 1) * BUF : 0);
         if (ch + 1 < NCH) gload(ch + 1);
         f4 acc1[HT][MT];
 #pragma unroll
         for (int ht = 0; ht < HT; ++ht)
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt) acc1[ht][mt] = f4{0.f, 0.f, 0.f, 0.f};
-        if constexpr (H16) {
+        if constexpr (X6) {
+#pragma unroll
+            for (int kk = 0; kk < KG / 2; ++kk) {
+                x8 xv[MT];
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt)
+                    xv[mt] = XS ? xs[XS ? mt : 0][XS ? kk : 0] : split8(xa[mt][2 * kk], xa[mt][2 * kk + 1]);
+#pragma unroll
+                for (int ht = 0; ht < HT; ++ht) {
+                    const x8 wv = ldx8(cur + (ht * 16 + li) * L0 + kk * 32 + lg * 8, HC * L0);
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt) acc1[ht][mt] = mfma6(wv, xv[mt], acc1[ht][mt]);
+                }
+            }
+        } else if constexpr (H16) {
 #pragma unroll
             for (int kk = 0; kk < KG / 2; ++kk)
 #pragma unroll
@@ -1203,7 +1377,19 @@ __global__ __launch_bounds__(NWV * 64) void k_mlp(MlpArgs a) {
 #pragma unroll
                 for (int r = 0; r < 4; ++r) acc1[ht][mt][r] = gelu_lut(gtab, acc1[ht][mt][r] + bb[r]);
         }
-        if constexpr (H16) {
+        if constexpr (X6) {
+#pragma unroll
+            for (int kb = 0; kb < HT / 2; ++kb)
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) {
+                    const x8 hv = split8(acc1[2 * kb][mt], acc1[2 * kb + 1][mt]);
+#pragma unroll
+                    for (int nt = 0; nt < NT; ++nt) {
+                        const x8 wv = ldx8(cur + NP * HC * L0 + (nt * 16 + li) * L2 + kb * 32 + lg * 8, T * L2);
+                        acc2[mt][nt] = mfma6(wv, hv, acc2[mt][nt]);
+                    }
+                }
+        } else if constexpr (H16) {
 #pragma unroll
             for (int kb = 0; kb < HT / 2; ++kb)
 #pragma unroll
@@ -1227,8 +1413,16 @@ __global__ __launch_bounds__(NWV * 64) void k_mlp(MlpArgs a) {
                         for (int mt = 0; mt < MT; ++mt) acc2[mt][nt] = mfma4(wv[r], acc1[ht][mt][r], acc2[mt][nt]);
                 }
         }
-        if (ch + 1 < NCH) lstore((ch + 1) & 1);
-        __syncthreads();
+        if constexpr (DB) {
+            if (ch + 1 < NCH) lstore((ch + 1) & 1);
+            __syncthreads();
+        } else {
+            __syncthreads();
+            if (ch + 1 < NCH) {
+                lstore(0);
+                __syncthreads();
+            }
+        }
     }
     // out^T = W2 H^T: each lane holds 4 consecutive output channels of one row.
 #pragma unroll
@@ -1256,11 +1450,21 @@ bool mlp(const MlpArgs& a, hipStream_t s, const char** why) {
         dim3 block{unsigned(threads), 1u, 1u};
         hipLaunchKernelGGL(kern, grid, block, 0, s, a);
     };
-    if (a.h0 && !a.h2) {
-        *why = "mlp: the fp16 path needs both k-permuted weights";
+    if ((a.h0 && !a.h2) || (a.x0 && !a.x2)) {
+        *why = "mlp: the 16-bit paths need both k-permuted weights";
         return false;
     }
     const bool h16 = a.h0 != nullptr;
+    if (a.x0 && !h16 && (a.t == 128 || a.t == 256)) {
+        // Split products: 8 waves of one row tile each share every streamed slice (three
+        // planes per matrix). t = 128: double-buffered (129 KB of LDS), the normalised rows
+        // kept in split form; t = 256: one buffer (126 KB), the rows split again per slice.
+        // Measured at 1080p (levels 2 and 3): t = 128 310 -> 197 us per launch against the
+        // fp32 products; t = 256 280 -> 264 us. Two row tiles per wave (8 or 4 waves) spill.
+        if (a.t == 128) go(k_mlp<128, 1, 32, true, 8, false, true, true>, 128, 512);
+        else go(k_mlp<256, 1, 32, true, 8, false, true, false, false>, 128, 512);
+        return true;
+    }
     switch (a.t) {
         case 32: h16 ? go(k_mlp<32, 4, 64, true>, 256) : go(k_mlp<32, 4, 64, false>, 256); break;
         case 64: h16 ? go(k_mlp<64, 2, 64, true>, 128) : go(k_mlp<64, 2, 64, false>, 128); break;
@@ -3113,8 +3317,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(T == 32 ? 2
 // weight load would feed a quarter as many products, and the separate MLP kernel, which
 // shares LDS-staged weights over 64 rows, measured faster.)
 // ---------------------------------------------------------------------------
-template <int T, bool MLP, bool H16>
+template <int T, bool MLP, bool H16, bool X6 = false>
 __global__ __launch_bounds__(T * 2) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_wmsa(MsaArgs a, long nw) {
+    // X6: split-operand products (fp32 LDS rows as in the fp32 path, split where loaded).
+    static_assert(!(X6 && H16), "the split products keep fp32 rows");
     constexpr int HEADS = T / 32, KG = T / 16, LDX = T + 8;
     // fp16 mode keeps the normalised tokens and the head outputs as k-permuted halves,
     // rows of PH = T + 16 (conflict-free 128-bit reads), inside the same arrays.
@@ -3189,7 +3395,33 @@ __global__ __launch_bounds__(T * 2) __attribute__((amdgpu_waves_per_eu(2, 2))) v
         for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
             for (int d = 0; d < 2; ++d) qf[mt][d] = kf[mt][d] = vf[mt][d] = f4{0.f, 0.f, 0.f, 0.f};
-        if constexpr (H16) {
+        if constexpr (X6) {
+            constexpr long PS = 3L * T * T;   // plane stride of the qkv weight
+            const __bf16* wq = a.xqkv + long(h * 32) * T;
+            const __bf16* wk = a.xqkv + long(T + h * 32) * T;
+            const __bf16* wv = a.xqkv + long(2 * T + h * 32) * T;
+#pragma unroll 1
+            for (int kk = 0; kk < KG / 2; ++kk) {
+                x8 xb[4];
+#pragma unroll
+                for (int mt = 0; mt < 4; ++mt) {
+                    const float* r = xs + (mt * 16 + li) * LDX + kk * 32 + lg * 4;
+                    xb[mt] = split8(ld4(r), ld4(r + 16));
+                }
+#pragma unroll
+                for (int d = 0; d < 2; ++d) {
+                    const x8 fq = ldx8(wq + (d * 16 + li) * T + kk * 32 + lg * 8, PS);
+                    const x8 fk = ldx8(wk + (d * 16 + li) * T + kk * 32 + lg * 8, PS);
+                    const x8 fv = ldx8(wv + (d * 16 + li) * T + kk * 32 + lg * 8, PS);
+#pragma unroll
+                    for (int mt = 0; mt < 4; ++mt) {
+                        qf[mt][d] = mfma6(fq, xb[mt], qf[mt][d]);
+                        kf[mt][d] = mfma6(fk, xb[mt], kf[mt][d]);
+                        vf[mt][d] = mfma6(xb[mt], fv, vf[mt][d]);
+                    }
+                }
+            }
+        } else if constexpr (H16) {
             const _Float16* wq = a.hqkv + long(h * 32) * T;
             const _Float16* wk = a.hqkv + long(T + h * 32) * T;
             const _Float16* wv = a.hqkv + long(2 * T + h * 32) * T;
@@ -3256,7 +3488,15 @@ __global__ __launch_bounds__(T * 2) __attribute__((amdgpu_waves_per_eu(2, 2))) v
         const float sc2 = a.scale * 1.4426950408889634f;   // logits in log2 units: p = 2^(l - max)
         const float* tab = a.tab + (long(h) * 64 + lane) * 64;
         h8 kh[H16 ? 4 : 1], qh[H16 ? 4 : 1], vh[H16 ? 2 : 1][2];
-        if constexpr (H16) {
+        x8 kx[X6 ? 4 : 1], vx[X6 ? 2 : 1][2];
+        if constexpr (X6) {
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt) kx[mt] = split8(kf[mt][0], kf[mt][1]);
+#pragma unroll
+            for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+                for (int nd = 0; nd < 2; ++nd) vx[kk][nd] = split8(vf[2 * kk][nd], vf[2 * kk + 1][nd]);
+        } else if constexpr (H16) {
 #pragma unroll
             for (int mt = 0; mt < 4; ++mt) {
                 kh[mt] = pack8(kf[mt][0], kf[mt][1]);
@@ -3272,7 +3512,11 @@ __global__ __launch_bounds__(T * 2) __attribute__((amdgpu_waves_per_eu(2, 2))) v
             f4 S[4];
 #pragma unroll
             for (int mt = 0; mt < 4; ++mt) S[mt] = f4{0.f, 0.f, 0.f, 0.f};
-            if constexpr (H16) {
+            if constexpr (X6) {
+                const x8 qx = split8(qf[nt][0], qf[nt][1]);
+#pragma unroll
+                for (int mt = 0; mt < 4; ++mt) S[mt] = mfma6(kx[mt], qx, S[mt]);
+            } else if constexpr (H16) {
 #pragma unroll
                 for (int mt = 0; mt < 4; ++mt) S[mt] = mfma16(kh[mt], qh[nt], S[mt]);
             } else {
@@ -3314,7 +3558,18 @@ __global__ __launch_bounds__(T * 2) __attribute__((amdgpu_waves_per_eu(2, 2))) v
             sum += __shfl_xor(sum, 32);
             const float inv = __builtin_amdgcn_rcpf(sum);
             f4 O[2] = {f4{0.f, 0.f, 0.f, 0.f}, f4{0.f, 0.f, 0.f, 0.f}};
-            if constexpr (H16) {
+            if constexpr (X6) {
+#pragma unroll
+                for (int kk = 0; kk < 2; ++kk) {
+                    const x8 px = split8(S[2 * kk], S[2 * kk + 1]);
+#pragma unroll
+                    for (int nd = 0; nd < 2; ++nd) O[nd] = mfma6(vx[kk][nd], px, O[nd]);
+                }
+                O[0] = O[0] * inv;
+                O[1] = O[1] * inv;
+#pragma unroll
+                for (int nd = 0; nd < 2; ++nd) st4(os + (nt * 16 + li) * LDX + h * 32 + nd * 16 + lg * 4, O[nd]);
+            } else if constexpr (H16) {
 #pragma unroll
                 for (int kk = 0; kk < 2; ++kk) {
                     const h8 ph = pack8(S[2 * kk], S[2 * kk + 1]);
@@ -3348,7 +3603,23 @@ __global__ __launch_bounds__(T * 2) __attribute__((amdgpu_waves_per_eu(2, 2))) v
     f4 acc[4][2];
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) acc[mt][0] = acc[mt][1] = f4{0.f, 0.f, 0.f, 0.f};
-    if constexpr (H16) {
+    if constexpr (X6) {
+#pragma unroll 2
+        for (int kk = 0; kk < KG / 2; ++kk) {
+            x8 ob[4];
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt) {
+                const float* r = os + (mt * 16 + li) * LDX + kk * 32 + lg * 4;
+                ob[mt] = split8(ld4(r), ld4(r + 16));
+            }
+#pragma unroll
+            for (int ct = 0; ct < 2; ++ct) {
+                const x8 fw = ldx8(a.xp + long(c0 + ct * 16 + li) * T + kk * 32 + lg * 8, long(T) * T);
+#pragma unroll
+                for (int mt = 0; mt < 4; ++mt) acc[mt][ct] = mfma6(fw, ob[mt], acc[mt][ct]);
+            }
+        }
+    } else if constexpr (H16) {
 #pragma unroll 4
         for (int kk = 0; kk < KG / 2; ++kk) {
             h8 ob[4];
@@ -3439,7 +3710,13 @@ __global__ __launch_bounds__(T * 2) __attribute__((amdgpu_waves_per_eu(2, 2))) v
 #pragma unroll
             for (int nt = 0; nt < KG; ++nt) acc2[i][nt] = f4{0.f, 0.f, 0.f, 0.f};
         h8 xnh[H16 ? MT : 1][H16 ? KG / 2 : 1];
-        if constexpr (H16) {
+        x8 xnx[X6 ? MT : 1][X6 ? KG / 2 : 1];
+        if constexpr (X6) {
+#pragma unroll
+            for (int i = 0; i < MT; ++i)
+#pragma unroll
+                for (int kk = 0; kk < KG / 2; ++kk) xnx[i][kk] = split8(xn[i][2 * kk], xn[i][2 * kk + 1]);
+        } else if constexpr (H16) {
 #pragma unroll
             for (int i = 0; i < MT; ++i)
 #pragma unroll
@@ -3452,7 +3729,16 @@ __global__ __launch_bounds__(T * 2) __attribute__((amdgpu_waves_per_eu(2, 2))) v
             for (int ht = 0; ht < HT; ++ht)
 #pragma unroll
                 for (int i = 0; i < MT; ++i) acc1[ht][i] = f4{0.f, 0.f, 0.f, 0.f};
-            if constexpr (H16) {
+            if constexpr (X6) {
+#pragma unroll
+                for (int kk = 0; kk < KG / 2; ++kk)
+#pragma unroll
+                    for (int ht = 0; ht < HT; ++ht) {
+                        const x8 wv = ldx8(a.x0 + long(ch * HC + ht * 16 + li) * T + kk * 32 + lg * 8, 4L * T * T);
+#pragma unroll
+                        for (int i = 0; i < MT; ++i) acc1[ht][i] = mfma6(wv, xnx[i][kk], acc1[ht][i]);
+                    }
+            } else if constexpr (H16) {
 #pragma unroll
                 for (int kk = 0; kk < KG / 2; ++kk)
 #pragma unroll
@@ -3481,7 +3767,15 @@ __global__ __launch_bounds__(T * 2) __attribute__((amdgpu_waves_per_eu(2, 2))) v
 #pragma unroll
                     for (int r = 0; r < 4; ++r) acc1[ht][i][r] = gelu_lut(gtab, acc1[ht][i][r] + bb[r]);
             }
-            if constexpr (H16) {
+            if constexpr (X6) {
+#pragma unroll
+                for (int i = 0; i < MT; ++i) {
+                    const x8 hv = split8(acc1[0][i], acc1[1][i]);
+#pragma unroll
+                    for (int nt = 0; nt < KG; ++nt)
+                        acc2[i][nt] = mfma6(ldx8(a.x2 + long(nt * 16 + li) * HID + ch * 32 + lg * 8, 4L * T * T), hv, acc2[i][nt]);
+                }
+            } else if constexpr (H16) {
                 // HC = 32 hidden units: k block ch of W2.
 #pragma unroll
                 for (int i = 0; i < MT; ++i) {
@@ -3517,6 +3811,17 @@ template <bool H16>
 static bool launch_msa(const MsaArgs& a, long nw, hipStream_t s, const char** why) {
     dim3 grid{unsigned((nw + 3) / 4), 1u, 1u}, block{256u, 1u, 1u};
     dim3 wgrid{unsigned(nw), 1u, 1u}, wblock{unsigned(a.t * 2), 1u, 1u};
+    if (!H16 && a.xqkv && a.xp && a.t >= 64 && (!a.w0 || (a.x0 && a.x2))) {
+        if (a.t == 64 && a.w0) hipLaunchKernelGGL((k_wmsa<64, true, false, true>), wgrid, wblock, 0, s, a, nw);
+        else if (a.t == 64) hipLaunchKernelGGL((k_wmsa<64, false, false, true>), wgrid, wblock, 0, s, a, nw);
+        else if (a.t == 128) hipLaunchKernelGGL((k_wmsa<128, false, false, true>), wgrid, wblock, 0, s, a, nw);
+        else if (a.t == 256) hipLaunchKernelGGL((k_wmsa<256, false, false, true>), wgrid, wblock, 0, s, a, nw);
+        else {
+            *why = "msa_fused: t must be 32, 64, 128 or 256";
+            return false;
+        }
+        return true;
+    }
     if (a.t == 32 && a.w0) hipLaunchKernelGGL((k_msa<32, true, H16>), grid, block, 0, s, a, nw);
     else if (a.t == 32) hipLaunchKernelGGL((k_msa<32, false, H16>), grid, block, 0, s, a, nw);
     else if (a.t == 64 && a.w0) hipLaunchKernelGGL((k_wmsa<64, true, H16>), wgrid, wblock, 0, s, a, nw);
@@ -3808,6 +4113,29 @@ void h16_permute(const float* src, half_t* dst, long rows, int K, hipStream_t s)
     if (n <= 0) return;
     dim3 grid{unsigned(std::min<long>((n + 255) / 256, 4096)), 1u, 1u}, block{256u, 1u, 1u};
     hipLaunchKernelGGL(k_h16_permute, grid, block, 0, s, src, dst, rows, K);
+}
+
+// The split weight planes: the same chunk order as k_h16_permute, parts h, m, l of every
+// element in planes rows * K elements apart (split8).
+__global__ void k_x6_permute(const float* __restrict__ src, __bf16* __restrict__ dst, long rows, int K) {
+    const long n = rows * (K / 8), ps = rows * long(K);
+    for (long i = long(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += long(gridDim.x) * blockDim.x) {
+        const long row = i / (K / 8);
+        const int q = int(i - row * (K / 8));
+        const float* p = src + row * K + 32 * (q >> 2) + 4 * (q & 3);
+        const x8 v = split8(ld4(p), ld4(p + 16));
+        __bf16* d = dst + row * K + q * 8;
+        stb8(d, v.h);
+        stb8(d + ps, v.m);
+        stb8(d + 2 * ps, v.l);
+    }
+}
+
+void x6_permute(const float* src, bf16_t* dst, long rows, int K, hipStream_t s) {
+    const long n = rows * (K / 8);
+    if (n <= 0) return;
+    dim3 grid{unsigned(std::min<long>((n + 255) / 256, 4096)), 1u, 1u}, block{256u, 1u, 1u};
+    hipLaunchKernelGGL(k_x6_permute, grid, block, 0, s, src, dst, rows, K);
 }
 
 __global__ void k_copy_f4(const f4* __restrict__ src, f4* __restrict__ dst, long n) {
