@@ -2909,24 +2909,41 @@ bool attention(const AttnArgs& a, hipStream_t s, const char** why) {
 //   3. x += out + bias, written back through the same index map (a permutation, so each
 //      window owns its 64 rows).
 // ---------------------------------------------------------------------------
-template <int T, bool MLP, bool H16>
+template <int T, bool MLP, bool H16, bool X6 = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(T == 32 ? 2 : 1, 2))) void k_msa(MsaArgs a, long nw) {
     constexpr int HEADS = T / 32, KG = T / 16, OT = T / 16;
+    // X6 (split-operand products, t = 32): the normalised tokens stay in registers in split
+    // form (at t = 32 a lane's LayerNorm output is exactly its operand of the q/k/v
+    // products), so the LDS holds only the MLP weights, as three bf16 planes each.
+    static_assert(!X6 || (!H16 && T == 32), "split products: t = 32, fp32 rows");
+    constexpr bool L16 = H16 || X6;   // 16-bit operand layout and pitches
     // Normalised tokens per wave: fp32 rows of T + 4 floats, or fp16 rows of T + 16 halves
     // in the k-permuted order of the f16 products.
     constexpr int LDX = H16 ? T + 16 : T + 4;
+    constexpr int XSF = X6 ? 0 : 4 * 64 * LDX;
     // MLP weights, resident for the whole workgroup: W0 [4T][T] and W2 [T][4T] with row
-    // pitches T + 8 and 4T + 8 floats (fp16: T + 16 and 4T + 16 halves, k-permuted), both
+    // pitches T + 8 and 4T + 8 floats (16-bit: T + 16 and 4T + 16 halves, k-permuted), both
     // conflict-free for 128-bit operand reads.
-    constexpr int HID = 4 * T, P0 = H16 ? T + 16 : T + 8, P2 = H16 ? HID + 16 : HID + 8;
-    constexpr int MLPF = MLP ? HID * P0 + T * P2 : 0;
-    using ET = std::conditional_t<H16, _Float16, float>;
-    __shared__ __align__(16) ET xs[4 * 64 * LDX + MLPF];
+    constexpr int HID = 4 * T, P0 = L16 ? T + 16 : T + 8, P2 = L16 ? HID + 16 : HID + 8;
+    constexpr int NP = X6 ? 3 : 1;
+    constexpr int MLPF = MLP ? NP * (HID * P0 + T * P2) : 0;
+    using ET = std::conditional_t<X6, __bf16, std::conditional_t<H16, _Float16, float>>;
+    __shared__ __align__(16) ET xs[XSF + MLPF + (XSF + MLPF == 0 ? 8 : 0)];
     __shared__ __align__(16) float gtab[MLP ? GELU_TABLE : 4];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    ET* const wm0 = xs + 4 * 64 * LDX;
-    ET* const wm2 = wm0 + HID * P0;
-    if constexpr (MLP) {
+    ET* const wm0 = xs + XSF;
+    ET* const wm2 = wm0 + NP * HID * P0;
+    if constexpr (MLP && X6) {
+        load_gelu_table(gtab, a.gelu, threadIdx.x, 256);
+        for (int f = threadIdx.x; f < NP * HID * T / 8; f += 256) {
+            const int p = f / (HID * T / 8), g = f % (HID * T / 8), r = g / (T / 8), c = g % (T / 8);
+            stb8(wm0 + p * HID * P0 + r * P0 + c * 8, ldb8(a.x0 + long(p) * HID * T + long(r) * T + c * 8));
+        }
+        for (int f = threadIdx.x; f < NP * T * HID / 8; f += 256) {
+            const int p = f / (HID * T / 8), g = f % (HID * T / 8), r = g / (HID / 8), c = g % (HID / 8);
+            stb8(wm2 + p * T * P2 + r * P2 + c * 8, ldb8(a.x2 + long(p) * HID * T + long(r) * HID + c * 8));
+        }
+    } else if constexpr (MLP) {
         load_gelu_table(gtab, a.gelu, threadIdx.x, 256);
         constexpr int EV = H16 ? 8 : 4;   // elements per 16-byte chunk
         const ET* g0 = H16 ? reinterpret_cast<const ET*>(a.h0) : reinterpret_cast<const ET*>(a.w0);
@@ -2952,7 +2969,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(T == 32 ? 2
     const int wr = valid ? int(unsigned(wi) - unsigned(img) * wpi) : 0;
     const int wh = int(unsigned(wr) / unsigned(a.nww)), ww = wr - wh * a.nww;
     const long ybase = long(img) * a.H;
-    ET* xw = xs + wave * 64 * LDX;
+    ET* xw = xs + (X6 ? 0 : wave * 64 * LDX);
     auto rowof = [&](int t) -> long {
         int y = wh * 8 + (t >> 3) + a.shift;
         int x = ww * 8 + (t & 7) + a.shift;
@@ -2964,6 +2981,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(T == 32 ? 2
     // 1. LN1 of the window's tokens into LDS. The raw rows stay in registers for the
     // attention residual (the wave is register-limited to two per SIMD either way).
     f4 xin[4][KG];
+    x8 xbx[X6 ? 4 : 1][X6 ? KG / 2 : 1];
     if (valid) {
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt) {
@@ -2991,7 +3009,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(T == 32 ? 2
                 f4 gg = ld4(a.ln_g + kg * 16 + lg * 4), bb = ld4(a.ln_b + kg * 16 + lg * 4);
                 v[kg] = (v[kg] - mu) * rs * gg + bb;
             }
-            if constexpr (H16) {
+            if constexpr (X6) {
+#pragma unroll
+                for (int kk = 0; kk < KG / 2; ++kk) xbx[mt][kk] = split8(v[2 * kk], v[2 * kk + 1]);
+            } else if constexpr (H16) {
 #pragma unroll
                 for (int kk = 0; kk < KG / 2; ++kk)
                     sth8(xw + (mt * 16 + li) * LDX + kk * 32 + lg * 8, pack8(v[2 * kk], v[2 * kk + 1]));
@@ -3021,7 +3042,27 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(T == 32 ? 2
         for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
             for (int d = 0; d < 2; ++d) qf[mt][d] = kf[mt][d] = vf[mt][d] = f4{0.f, 0.f, 0.f, 0.f};
-        if constexpr (H16) {
+        if constexpr (X6) {
+            constexpr long PS = 3L * T * T;
+            const __bf16* wq = a.xqkv + long(h * 32) * T;
+            const __bf16* wk = a.xqkv + long(T + h * 32) * T;
+            const __bf16* wv = a.xqkv + long(2 * T + h * 32) * T;
+#pragma unroll
+            for (int kk = 0; kk < KG / 2; ++kk) {
+#pragma unroll
+                for (int d = 0; d < 2; ++d) {
+                    const x8 fq = ldx8(wq + (d * 16 + li) * T + kk * 32 + lg * 8, PS);
+                    const x8 fk = ldx8(wk + (d * 16 + li) * T + kk * 32 + lg * 8, PS);
+                    const x8 fv = ldx8(wv + (d * 16 + li) * T + kk * 32 + lg * 8, PS);
+#pragma unroll
+                    for (int mt = 0; mt < 4; ++mt) {
+                        qf[mt][d] = mfma6(fq, xbx[mt][kk], qf[mt][d]);
+                        kf[mt][d] = mfma6(fk, xbx[mt][kk], kf[mt][d]);
+                        vf[mt][d] = mfma6(xbx[mt][kk], fv, vf[mt][d]);
+                    }
+                }
+            }
+        } else if constexpr (H16) {
             const _Float16* wq = a.hqkv + long(h * 32) * T;
             const _Float16* wk = a.hqkv + long(T + h * 32) * T;
             const _Float16* wv = a.hqkv + long(2 * T + h * 32) * T;
@@ -3086,7 +3127,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(T == 32 ? 2
         // fp16 operands of S^T = K Q^T (the head's 32 dims are one k block) and of
         // O^T = V^T P^T (keys 32kk .. 32kk + 31 are k block kk).
         h8 kh[H16 ? 4 : 1], qh[H16 ? 4 : 1], vh[H16 ? 2 : 1][2];
-        if constexpr (H16) {
+        x8 kx[X6 ? 4 : 1], vx[X6 ? 2 : 1][2];
+        if constexpr (X6) {
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt) kx[mt] = split8(kf[mt][0], kf[mt][1]);
+#pragma unroll
+            for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+                for (int nd = 0; nd < 2; ++nd) vx[kk][nd] = split8(vf[2 * kk][nd], vf[2 * kk + 1][nd]);
+        } else if constexpr (H16) {
 #pragma unroll
             for (int mt = 0; mt < 4; ++mt) {
                 kh[mt] = pack8(kf[mt][0], kf[mt][1]);
@@ -3102,7 +3151,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(T == 32 ? 2
             f4 S[4];
 #pragma unroll
             for (int mt = 0; mt < 4; ++mt) S[mt] = f4{0.f, 0.f, 0.f, 0.f};
-            if constexpr (H16) {
+            if constexpr (X6) {
+                const x8 qx = split8(qf[nt][0], qf[nt][1]);
+#pragma unroll
+                for (int mt = 0; mt < 4; ++mt) S[mt] = mfma6(kx[mt], qx, S[mt]);
+            } else if constexpr (H16) {
 #pragma unroll
                 for (int mt = 0; mt < 4; ++mt) S[mt] = mfma16(kh[mt], qh[nt], S[mt]);
             } else {
@@ -3144,7 +3197,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(T == 32 ? 2
             sum += __shfl_xor(sum, 32);
             const float inv = __builtin_amdgcn_rcpf(sum);
             f4 O[2] = {f4{0.f, 0.f, 0.f, 0.f}, f4{0.f, 0.f, 0.f, 0.f}};
-            if constexpr (H16) {
+            if constexpr (X6) {
+#pragma unroll
+                for (int kk = 0; kk < 2; ++kk) {
+                    const x8 px = split8(S[2 * kk], S[2 * kk + 1]);
+#pragma unroll
+                    for (int nd = 0; nd < 2; ++nd) O[nd] = mfma6(vx[kk][nd], px, O[nd]);
+                }
+                O[0] = O[0] * inv;
+                O[1] = O[1] * inv;
+                const x8 ox = split8(O[0], O[1]);
+#pragma unroll
+                for (int ot = 0; ot < OT; ++ot)
+                    acc[nt][ot] = mfma6(ldx8(a.xp + long(ot * 16 + li) * T + h * 32 + lg * 8, long(T) * T), ox, acc[nt][ot]);
+            } else if constexpr (H16) {
 #pragma unroll
                 for (int kk = 0; kk < 2; ++kk) {
                     const h8 ph = pack8(S[2 * kk], S[2 * kk + 1]);
@@ -3221,7 +3287,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(T == 32 ? 2
 #pragma unroll
             for (int nt = 0; nt < OT; ++nt) acc2[mt][nt] = f4{0.f, 0.f, 0.f, 0.f};
         h8 xnh[H16 ? 4 : 1][H16 ? OT / 2 : 1];
-        if constexpr (H16) {
+        x8 xnx[X6 ? 4 : 1][X6 ? OT / 2 : 1];
+        if constexpr (X6) {
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+                for (int kk = 0; kk < OT / 2; ++kk) xnx[mt][kk] = split8(xn[mt][2 * kk], xn[mt][2 * kk + 1]);
+        } else if constexpr (H16) {
 #pragma unroll
             for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
@@ -3234,7 +3306,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(T == 32 ? 2
             for (int ht = 0; ht < HT; ++ht)
 #pragma unroll
                 for (int mt = 0; mt < 4; ++mt) acc1[ht][mt] = f4{0.f, 0.f, 0.f, 0.f};
-            if constexpr (H16) {
+            if constexpr (X6) {
+#pragma unroll
+                for (int kk = 0; kk < OT / 2; ++kk)
+#pragma unroll
+                    for (int ht = 0; ht < HT; ++ht) {
+                        const x8 wv = ldx8(wm0 + (ch * HC + ht * 16 + li) * P0 + kk * 32 + lg * 8, HID * P0);
+#pragma unroll
+                        for (int mt = 0; mt < 4; ++mt) acc1[ht][mt] = mfma6(wv, xnx[mt][kk], acc1[ht][mt]);
+                    }
+            } else if constexpr (H16) {
 #pragma unroll
                 for (int kk = 0; kk < OT / 2; ++kk)
 #pragma unroll
@@ -3263,7 +3344,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(T == 32 ? 2
 #pragma unroll
                     for (int r = 0; r < 4; ++r) acc1[ht][mt][r] = gelu_lut(gtab, acc1[ht][mt][r] + bb[r]);
             }
-            if constexpr (H16) {
+            if constexpr (X6) {
+#pragma unroll
+                for (int mt = 0; mt < 4; ++mt) {
+                    const x8 hv = split8(acc1[0][mt], acc1[1][mt]);
+#pragma unroll
+                    for (int nt = 0; nt < OT; ++nt)
+                        acc2[mt][nt] = mfma6(ldx8(wm2 + (nt * 16 + li) * P2 + ch * 32 + lg * 8, T * P2), hv, acc2[mt][nt]);
+                }
+            } else if constexpr (H16) {
                 // HC = 32 hidden units: k block ch of W2.
 #pragma unroll
                 for (int mt = 0; mt < 4; ++mt) {
@@ -3811,8 +3900,10 @@ template <bool H16>
 static bool launch_msa(const MsaArgs& a, long nw, hipStream_t s, const char** why) {
     dim3 grid{unsigned((nw + 3) / 4), 1u, 1u}, block{256u, 1u, 1u};
     dim3 wgrid{unsigned(nw), 1u, 1u}, wblock{unsigned(a.t * 2), 1u, 1u};
-    if (!H16 && a.xqkv && a.xp && a.t >= 64 && (!a.w0 || (a.x0 && a.x2))) {
-        if (a.t == 64 && a.w0) hipLaunchKernelGGL((k_wmsa<64, true, false, true>), wgrid, wblock, 0, s, a, nw);
+    if (!H16 && a.xqkv && a.xp && (!a.w0 || (a.x0 && a.x2))) {
+        if (a.t == 32 && a.w0) hipLaunchKernelGGL((k_msa<32, true, false, true>), grid, block, 0, s, a, nw);
+        else if (a.t == 32) hipLaunchKernelGGL((k_msa<32, false, false, true>), grid, block, 0, s, a, nw);
+        else if (a.t == 64 && a.w0) hipLaunchKernelGGL((k_wmsa<64, true, false, true>), wgrid, wblock, 0, s, a, nw);
         else if (a.t == 64) hipLaunchKernelGGL((k_wmsa<64, false, false, true>), wgrid, wblock, 0, s, a, nw);
         else if (a.t == 128) hipLaunchKernelGGL((k_wmsa<128, false, false, true>), wgrid, wblock, 0, s, a, nw);
         else if (a.t == 256) hipLaunchKernelGGL((k_wmsa<256, false, false, true>), wgrid, wblock, 0, s, a, nw);
