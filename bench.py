@@ -11,9 +11,12 @@ contract with pad and crop fused into the first and last convolution).
 value = 1920*1080 input pixels / mean step time, in Mpx/s (the reference counts input
 pixels, examples/bench.rs:191). Per-kernel device times come from HIP event pairs that
 the library records around every launch on its own stream during the timed steps; the
-fp16-operand mode is timed after them and reported in its own sub-object (fp16_mode).
+fp16-operand mode is timed after them and reported in its own sub-object (fp16_mode), as is
+the all-fp32-MFMA mode (fp32_mfma_mode). The default fp32 mode forms most products from an
+exact three-way bf16 split of the fp32 operands on the bf16 matrix cores (SPLIT_CLASSES).
 
 Usage: python bench.py [--gpus 1] [--steps 10] [--warmup 5] [--no-cpu-baseline] [--no-fp16]
+                       [--no-fp32-mfma]
 """
 import argparse
 import json
@@ -27,12 +30,21 @@ sys.path.insert(0, os.path.join(REPO, "scunet-rs_amd"))
 METRIC = "megapixels/sec end-to-end SCUNet-color 1920x1088; attention kernel TFLOP/s"
 PEAK_FP32_TFLOPS = 157.3      # MI355X dense fp32 matrix
 PEAK_FP16_TFLOPS = 2500.0     # MI355X dense fp16 matrix (the fp16-operand mode's products)
+PEAK_BF16_TFLOPS = 2500.0     # MI355X dense bf16 matrix (the split-operand fp32 products)
 PEAK_HBM_GBS = 8000.0         # MI355X HBM3E
 # The 3x3 convolutions run as Winograd F(2x2,3x3) unless SCUNET_HIP_DIRECT3X3 is set (or in
 # the fp16 mode, which uses a direct kernel): the library counts the direct convolution's
 # 18*cin*cout FLOP per pixel for every path, the Winograd kernel executes 16 products of
 # (cout x cin) per 2x2 output tile, i.e. 8*cin*cout FLOP per pixel, on the MFMA units.
 WINOGRAD_EXECUTED = 8.0 / 18.0
+# The default fp32 mode forms these classes' products from an exact three-way bf16 split of
+# both fp32 operands: six bf16 part products per fp32 multiply-add on the bf16 matrix cores
+# (fp32 accumulation). Their executed work is 6x the algorithmic FLOP, against the bf16 peak.
+SPLIT_CLASSES = {"conv1x1", "conv1x1_chain", "mlp_fused", "msa_fused", "tblock_fused", "up2x2", "down2x2"}
+SPLIT_EXECUTED = 6.0
+PRODUCTS = ("fp32 operands, planes and accumulation; the products of the split classes (" +
+            ", ".join(sorted(SPLIT_CLASSES)) + ") on the bf16 matrix cores from an exact three-way bf16 split "
+            "of each operand (six part products, dropped terms < 2^-25 |ab|), the rest on the fp32 matrix cores")
 
 
 def log(*a):
@@ -57,9 +69,10 @@ def roofline_of(name, launches, ms, flop, byts, peak_tflops=PEAK_FP32_TFLOPS, ex
                 frac=round(ach / PEAK_HBM_GBS, 4))
 
 
-def class_table(rows, steps, peak_tflops, winograd):
+def class_table(rows, steps, peak_tflops, winograd, split=frozenset()):
     """Per kernel class (rows are per class and UNet level "@Lk"): roofline figures, share of
-    device time and the per-level breakdown, sorted by device time."""
+    device time and the per-level breakdown, sorted by device time. Classes in `split` run
+    split-operand products: executed FLOP 6x the algorithmic, against the bf16 peak."""
     total_ms = max(sum(r[2] for r in rows), 1e-9)
     classes = {}
     for name, n, ms, flop, byts in rows:
@@ -71,8 +84,14 @@ def class_table(rows, steps, peak_tflops, winograd):
     out = []
     for base, (n, ms, flop, byts) in sorted(classes.items(), key=lambda kv: -kv[1][1]):
         ex = WINOGRAD_EXECUTED if (winograd and base == "conv3x3") else 1.0
-        k = roofline_of(base, n, ms, flop, byts, peak_tflops, ex)
+        pk = peak_tflops
+        if base in split:
+            ex, pk = SPLIT_EXECUTED, PEAK_BF16_TFLOPS
+        k = roofline_of(base, n, ms, flop, byts, pk, ex)
         k["share"] = round(ms / total_ms, 4)
+        if base in split:
+            k["products"] = "split bf16 x6: achieved/frac count the six bf16 part products per fp32 multiply-add"
+            k["fp32_equiv_tflops"] = round(flop / (ms * 1e-3) / 1e12, 3)
         if ex != 1.0:
             k["algorithm"] = ("winograd F(2x2,3x3): achieved/frac count the 8*cin*cout FLOP per pixel the MFMA "
                               "units execute; direct_equiv_tflops counts the direct convolution's 18*cin*cout")
@@ -80,7 +99,7 @@ def class_table(rows, steps, peak_tflops, winograd):
         k["levels"] = {}
         for name, n2, ms2, flop2, byts2 in rows:
             if name.split("@")[0] == base and "@" in name:
-                lv = roofline_of(name, n2, ms2, flop2, byts2, peak_tflops, ex)
+                lv = roofline_of(name, n2, ms2, flop2, byts2, pk, ex)
                 k["levels"][name.split("@")[1]] = {"achieved": lv["achieved"], "unit": lv["unit"],
                                                    "frac": lv["frac"], "avg_launch_ms": lv["avg_launch_ms"],
                                                    "ms_per_step": round(ms2 / steps, 4)}
@@ -190,6 +209,7 @@ def main():
                     help="time the steps without the per-launch event pairs")
     ap.add_argument("--no-attn-sweep", action="store_true", help="skip the config-5 attention sweep")
     ap.add_argument("--no-fp16", action="store_true", help="skip the fp16-operand mode's line")
+    ap.add_argument("--no-fp32-mfma", action="store_true", help="skip the all-fp32-MFMA mode's line")
     ap.add_argument("--profile-fp16", action="store_true", help="with --profile-pass: the forward in the fp16 mode")
     ap.add_argument("--profile-pass", action="store_true",
                     help="for rocprofv3 counter runs: one forward plus one 256 MiB device copy (the "
@@ -274,6 +294,28 @@ def main():
     log(f"bench: host to host (scunet_hip_run, PCIe included) {h2h_med * 1e3:.2f} ms, {h * w / h2h_med / 1e6:.2f} Mpx/s")
     fp = be.footprint()
 
+    # The all-fp32-MFMA mode (SCUNET_HIP_FP32_MFMA: every product on the fp32 matrix cores),
+    # timed the same way and reported beside the default, with its difference from it.
+    mfma_mode = None
+    if not args.no_fp32_mfma:
+        be.set_precision("fp32_mfma")
+        for _ in range(args.warmup):
+            be.run_device(xp, c, h, w, yp)
+        be.synchronize()
+        t1 = time.perf_counter()
+        for _ in range(args.steps):
+            be.run_device(xp, c, h, w, yp)
+        be.synchronize()
+        dtm = (time.perf_counter() - t1) / args.steps
+        ym = be.d2h(np.empty_like(x), yp)
+        be.set_precision("fp32")
+        mfma_mode = {"value": round(h * w / dtm / 1e6, 3), "unit": "Mpx/s", "ms_per_step": round(dtm * 1e3, 3),
+                     "max_abs_vs_default": float(np.abs(ym.astype(np.float64) - y.astype(np.float64)).max()),
+                     "note": "scunet_hip_set_precision(SCUNET_HIP_FP32_MFMA): every product on the fp32 matrix "
+                             "cores (v_mfma_f32_16x16x4_f32); same planes and accumulation as the default"}
+        log(f"bench: fp32-MFMA mode {dtm * 1e3:.2f} ms/step, {mfma_mode['value']:.2f} Mpx/s, max |diff| vs default "
+            f"{mfma_mode['max_abs_vs_default']:.2e}")
+
     # The fp16-operand mode (fp16 MFMA operands, fp32 accumulation and planes), reported
     # beside the fp32 headline with its error against the fp32 output of the same input.
     fp16 = None
@@ -323,7 +365,8 @@ def main():
             log(f"bench: fp16 mode forward {f['tflops']} TFLOP/s ({100 * f['frac_of_fp16_peak']:.1f}% of the fp16 "
                 f"peak), {f['algorithmic_gbs']} GB/s ({100 * f['frac_of_hbm']:.1f}% of HBM)")
 
-    kernels = class_table(rows, args.steps, PEAK_FP32_TFLOPS, winograd=not os.environ.get("SCUNET_HIP_DIRECT3X3"))
+    kernels = class_table(rows, args.steps, PEAK_FP32_TFLOPS, winograd=not os.environ.get("SCUNET_HIP_DIRECT3X3"),
+                          split=SPLIT_CLASSES)
     for k in kernels:
         log(f"  {k['kernel']:>14}: {k['launches']:5d} launches, {k['avg_launch_ms'] * 1e3:9.1f} us avg, "
             f"{k['achieved']:9.2f} {k['unit']} ({100 * k['frac']:.1f}% of {k['bound']}), share {100 * k['share']:.1f}%")
@@ -377,6 +420,7 @@ def main():
         "config": {"workload": "SCUNet-color whole-image forward, 1x3x1080x1920 replicate-padded to 1088x1920 "
                                "(benchmark config 3), device-resident input, pad+crop on device",
                    "in_nc": 3, "dim": 64, "blocks": [4] * 7, "window": 8, "head_dim": 32,
+                   "products": PRODUCTS,
                    "kernel_events": not args.no_kernel_events},
         "roofline": dominant,
         "attention_tflops": attn_tflops,
@@ -391,6 +435,7 @@ def main():
                          "note": "scunet_hip_run on host buffers: H2D + pad + forward + crop + D2H, median of 3"},
         "device_bytes": {"weights": fp[0], "scratch": fp[1]},
         "fp16_mode": fp16,
+        "fp32_mfma_mode": mfma_mode,
     }
     be.free(xp)
     be.free(yp)

@@ -81,7 +81,13 @@ int scunet_hip_arch(const scunet_hip* h, int* in_nc, int* dim, int* head_dim, in
 const char* scunet_hip_variant(const scunet_hip* h);
 
 /* --- arithmetic mode (no counterpart in the reference, whose GPU path is fp32 only) ---
- * SCUNET_HIP_FP32 (the default): every product in fp32, the reference's arithmetic.
+ * SCUNET_HIP_FP32 (the default): fp32 operands, planes and accumulation, the reference's
+ * arithmetic to fp32 rounding. Where a kernel has the form, a matrix product runs on the
+ * bf16 matrix cores from an exact three-way bf16 split of each fp32 operand (x = h + m + l
+ * exactly) as the six part products that can exceed 2^-24 |ab|, accumulated in fp32; the
+ * three dropped are below 2^-25 |ab| together, less than fp32's own rounding of one
+ * product. The other products run on the fp32 matrix cores.
+ * SCUNET_HIP_FP32_MFMA: every product on the fp32 matrix cores (v_mfma_f32_16x16x4_f32).
  * SCUNET_HIP_FP16: the matrix products take fp16 operands (round to nearest even) with fp32
  * accumulation; planes, residuals, LayerNorm, softmax and GELU stay fp32. Faster, and
  * within a stated looser tolerance of the fp32 result (max abs error and PSNR against
@@ -89,6 +95,7 @@ const char* scunet_hip_variant(const scunet_hip* h);
  * The mode applies to the handle's following calls. */
 #define SCUNET_HIP_FP32 0
 #define SCUNET_HIP_FP16 1
+#define SCUNET_HIP_FP32_MFMA 2
 int scunet_hip_set_precision(scunet_hip* h, int mode);
 /* The handle's mode, or -1 for a null handle. */
 int scunet_hip_precision(const scunet_hip* h);

@@ -111,8 +111,9 @@ struct scunet_hip {
     size_t h16bytes = 0;
     std::map<std::string, const half_t*> hw;
     std::map<const float*, const half_t*> hw_of;   // fp32 device pointer -> its fp16 copy
-    // The split-operand fp32 products (x6): three bf16 part planes per matrix weight, built
-    // at create; x6 = false sends every fp32 product to the fp32 matrix cores instead.
+    // The split-operand fp32 products (x6, the default fp32 mode): three bf16 part planes per
+    // matrix weight, built at create; x6 = false (SCUNET_HIP_FP32_MFMA) sends every fp32
+    // product to the fp32 matrix cores instead.
     bool x6 = false;
     bf16_t* x6blob = nullptr;
     size_t x6bytes = 0;
@@ -479,7 +480,7 @@ bool msa_unfused(scunet_hip* h, const std::string& p, float* yt, int c, int t, i
         AttnArgs a;
         a.qkv = s.qkv; a.ldq = 3 * t; a.out = s.o; a.ldo = t; a.tab = h->atab[p];
         a.C = t; a.heads = t / h->wt.head_dim; a.nwh = H / 8; a.nww = Wd / 8; a.H = H; a.W = Wd;
-        a.shift = shift; a.pixel_mode = 1; a.scale = h->scale; a.wide = h->attn64; a.qsplit = h->attn_qs;
+        a.shift = shift; a.pixel_mode = 1; a.scale = h->scale; a.wide = h->attn64; a.qsplit = h->attn_qs; a.split = !h->h16 && h->x6;
         long nw = long(a.nwh) * a.nww;
         Span sp(h, "attention", 16384.0 * t * nw, 4.0 * 64.0 * nw * 4 * t);
         const char* why = nullptr;
@@ -963,13 +964,11 @@ static int create_handle(const char* path, const scunet_hip_arch_info* arch, scu
         g_create_error = h->err;
         return 1;
     }
-    // A/B switch (development): fp32 products in split form where a kernel has one.
-    if (std::getenv("SCUNET_HIP_X6") != nullptr) {
-        h->x6 = true;
-        if (!build_x6_weights(h.get())) {
-            g_create_error = h->err;
-            return 1;
-        }
+    // The default fp32 mode forms products from split operands where a kernel can.
+    h->x6 = true;
+    if (!build_x6_weights(h.get())) {
+        g_create_error = h->err;
+        return 1;
     }
     if (arch) h->wt.forget_data();   // the caller's buffers are not ours beyond this call
     *out = h.release();
@@ -984,21 +983,27 @@ const char* scunet_hip_name(const scunet_hip*) { return "hip"; }
 
 int scunet_hip_set_precision(scunet_hip* h, int mode) {
     if (!h) return 1;
-    if (mode != SCUNET_HIP_FP32 && mode != SCUNET_HIP_FP16) {
-        fail(h, "scunet_hip_set_precision: mode must be SCUNET_HIP_FP32 (0) or SCUNET_HIP_FP16 (1)");
+    if (mode != SCUNET_HIP_FP32 && mode != SCUNET_HIP_FP16 && mode != SCUNET_HIP_FP32_MFMA) {
+        fail(h, "scunet_hip_set_precision: mode must be SCUNET_HIP_FP32 (0), SCUNET_HIP_FP16 (1) or "
+                "SCUNET_HIP_FP32_MFMA (2)");
         return 1;
     }
     try {
         if (mode == SCUNET_HIP_FP16 && !build_h16_weights(h)) return 1;
+        if (mode == SCUNET_HIP_FP32 && !build_x6_weights(h)) return 1;
     } catch (const std::exception& e) {
         fail(h, std::string("scunet_hip_set_precision: ") + e.what());
         return 1;
     }
-    h->h16 = mode;
+    h->h16 = mode == SCUNET_HIP_FP16 ? 1 : 0;
+    h->x6 = mode == SCUNET_HIP_FP32;
     return 0;
 }
 
-int scunet_hip_precision(const scunet_hip* h) { return h ? h->h16 : -1; }
+int scunet_hip_precision(const scunet_hip* h) {
+    if (!h) return -1;
+    return h->h16 ? SCUNET_HIP_FP16 : h->x6 ? SCUNET_HIP_FP32 : SCUNET_HIP_FP32_MFMA;
+}
 
 int scunet_hip_arch(const scunet_hip* h, int* in_nc, int* dim, int* head_dim, int* window, int* config) {
     if (!h) return -1;
@@ -1409,7 +1414,7 @@ int scunet_hip_attention_kernel_probe(scunet_hip* h, size_t hh, size_t ww, size_
         AttnArgs a;
         a.qkv = dq; a.ldq = long(3 * c); a.out = y; a.ldo = long(c); a.tab = dt; a.C = int(c); a.heads = int(heads);
         a.nwh = int(hh / 8); a.nww = int(ww / 8); a.H = int(hh); a.W = int(ww); a.shift = int(shift);
-        a.pixel_mode = 0; a.scale = std::pow(float(hd), -0.5f); a.wide = h->attn64; a.qsplit = h->attn_qs;
+        a.pixel_mode = 0; a.scale = std::pow(float(hd), -0.5f); a.wide = h->attn64; a.qsplit = h->attn_qs; a.split = !h->h16 && h->x6;
         const char* why = nullptr;
         if (!attention(a, h->stream, &why)) return fail(h, why);
         if (!launched(h, "attention probe")) return false;
@@ -1479,7 +1484,7 @@ int scunet_hip_attention_probe(scunet_hip* h, const char* prefix, size_t hh, siz
         AttnArgs a;
         a.qkv = qkv; a.ldq = 3 * t; a.out = att; a.ldo = t; a.tab = h->atab[prefix]; a.C = t;
         a.heads = t / h->wt.head_dim; a.nwh = int(hh / 8); a.nww = int(ww / 8); a.H = int(hh); a.W = int(ww);
-        a.shift = int(shift); a.pixel_mode = 1; a.scale = h->scale; a.wide = h->attn64; a.qsplit = h->attn_qs;
+        a.shift = int(shift); a.pixel_mode = 1; a.scale = h->scale; a.wide = h->attn64; a.qsplit = h->attn_qs; a.split = !h->h16 && h->x6;
         const char* why = nullptr;
         if (!attention(a, h->stream, &why)) return fail(h, why);
         g = GemmArgs{};
@@ -1503,7 +1508,7 @@ int scunet_hip_bench_attn(scunet_hip* h, const float* qkv, const float* rp, floa
         AttnArgs a;
         a.qkv = qkv; a.ldq = long(3 * c); a.out = out; a.ldo = long(c); a.tab = dt; a.C = int(c);
         a.heads = int(heads); a.nwh = int(nwh); a.nww = int(nww); a.H = int(nwh * 8); a.W = int(nww * 8);
-        a.shift = int(shift); a.pixel_mode = 0; a.scale = h->scale; a.wide = h->attn64; a.qsplit = h->attn_qs;
+        a.shift = int(shift); a.pixel_mode = 0; a.scale = h->scale; a.wide = h->attn64; a.qsplit = h->attn_qs; a.split = !h->h16 && h->x6;
         const char* why = nullptr;
         for (int i = 0; i < 3; ++i)
             if (!attention(a, h->stream, &why)) return fail(h, why);

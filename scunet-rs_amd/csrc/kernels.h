@@ -187,6 +187,7 @@ struct AttnArgs {
     float scale = 0.f;
     int wide = 0;                  // 1: 64-bit element offsets even where 32-bit ones would do
     int qsplit = 0;                // query parts per (window, head): 0 automatic, 1 or 2
+    int split = 0;                 // 1: split-operand products (the default fp32 mode)
 };
 // 8x8 windows, head_dim 32, at most 8 heads.
 bool attention(const AttnArgs& a, hipStream_t s, const char** why);

@@ -2715,8 +2715,8 @@ void winograd_filter_slices(const float* u, int cout, int cin, float* u8) {
 // loads, 64 contiguous bytes per key), so the only LDS is the 7.2 KB of tables and the
 // kernel fits in 128 VGPRs: four waves per SIMD, 4 096 (window, head) units in flight.
 // ---------------------------------------------------------------------------
-template <bool WIDE, int QS>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4))) void k_attention(AttnArgs a, long units) {
+template <bool WIDE, int QS, bool X6 = false>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(X6 ? 2 : 4, X6 ? 2 : 4))) void k_attention(AttnArgs a, long units) {
     // Element offsets: 32-bit (WIDE = false) unless the qkv plane reaches 2^32 elements.
     using U = typename std::conditional<WIDE, unsigned long, unsigned>::type;
     __shared__ float rps[8 * 225];                // log2(e) * rel-pos tables, all heads
@@ -2783,7 +2783,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
     // All of the window-head's operands are requested before the first product.
     // kf / qf: token 16m + li, dims 16G + 4lg .. +3. vv: the A operand of O^T = V^T P^T,
     // dim 16nd + li against keys 16kt + 4lg + r.
+    // X6 (split-operand products): K and V go to split form once (the 16-bit operand layout:
+    // key block kk of V^T is key tiles 2kk, 2kk + 1), each query tile before its product.
     f4 kf[4][2], qf[NQ][2], vv[4][2];
+    x8 kx[X6 ? 4 : 1], vsx[X6 ? 2 : 1][2];
 #pragma unroll
     for (int m = 0; m < 4; ++m)
 #pragma unroll
@@ -2798,6 +2801,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
         for (int nd = 0; nd < 2; ++nd)
 #pragma unroll
             for (int r = 0; r < 4; ++r) vv[kt][nd][r] = v_base[(vy[kt] + vx[r]) * U(a.ldq) + 16 * nd];
+    if constexpr (X6) {
+#pragma unroll
+        for (int m = 0; m < 4; ++m) kx[m] = split8(kf[m][0], kf[m][1]);
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+            for (int nd = 0; nd < 2; ++nd) vsx[kk][nd] = split8(vv[2 * kk][nd], vv[2 * kk + 1][nd]);
+    }
     // Bias: query p = 16nt + li and key q = 16mt + 4lg + r give table entry
     // (p/8 - q/8 + 7) * 15 + (p%8 - q%8 + 7) = base + 30 (nt - mt) - r (cpu.rs:532-546);
     // read from LDS where each logit is formed.
@@ -2818,12 +2829,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
         f4 S[4];
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt) S[mt] = f4{0.f, 0.f, 0.f, 0.f};
+        if constexpr (X6) {
+            const x8 qx = split8(qf[j][0], qf[j][1]);
 #pragma unroll
-        for (int G = 0; G < 2; ++G)
+            for (int mt = 0; mt < 4; ++mt) S[mt] = mfma6(kx[mt], qx, S[mt]);
+        } else {
 #pragma unroll
-            for (int s4 = 0; s4 < 4; ++s4)
+            for (int G = 0; G < 2; ++G)
 #pragma unroll
-                for (int mt = 0; mt < 4; ++mt) S[mt] = mfma4(kf[mt][G][s4], qf[j][G][s4], S[mt]);
+                for (int s4 = 0; s4 < 4; ++s4)
+#pragma unroll
+                    for (int mt = 0; mt < 4; ++mt) S[mt] = mfma4(kf[mt][G][s4], qf[j][G][s4], S[mt]);
+        }
         // Logits for query 16nt + li against keys 16mt + 4lg + r.
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt)
@@ -2859,12 +2876,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
         // consecutive keys: the B operand as they stand), then O / sum: each lane ends with
         // dims 16nd + 4lg .. +3 of query 16nt + li.
         f4 O[2] = {f4{0.f, 0.f, 0.f, 0.f}, f4{0.f, 0.f, 0.f, 0.f}};
+        if constexpr (X6) {
 #pragma unroll
-        for (int kt = 0; kt < 4; ++kt)
+            for (int kk = 0; kk < 2; ++kk) {
+                const x8 px = split8(S[2 * kk], S[2 * kk + 1]);
 #pragma unroll
-            for (int r = 0; r < 4; ++r)
+                for (int nd = 0; nd < 2; ++nd) O[nd] = mfma6(vsx[kk][nd], px, O[nd]);
+            }
+        } else {
 #pragma unroll
-                for (int nd = 0; nd < 2; ++nd) O[nd] = mfma4(vv[kt][nd][r], S[kt][r], O[nd]);
+            for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+#pragma unroll
+                    for (int nd = 0; nd < 2; ++nd) O[nd] = mfma4(vv[kt][nd][r], S[kt][r], O[nd]);
+        }
         const float inv = 1.0f / sum;
         float* o = a.out + long(row_of(nt)) * a.ldo + hoff + lg * 4;
         st4(o, O[0] * inv);
@@ -2887,7 +2913,15 @@ bool attention(const AttnArgs& a, hipStream_t s, const char** why) {
     const int qs = a.qsplit ? a.qsplit : (wheads <= 4096 ? 2 : 1);
     const long units = wheads * qs;
     dim3 grid(unsigned((units + 3) / 4));
-    if (qs == 2) {
+    if (a.split) {
+        if (qs == 2) {
+            if (wide) hipLaunchKernelGGL((k_attention<true, 2, true>), grid, dim3(256), 0, s, a, units);
+            else hipLaunchKernelGGL((k_attention<false, 2, true>), grid, dim3(256), 0, s, a, units);
+        } else {
+            if (wide) hipLaunchKernelGGL((k_attention<true, 1, true>), grid, dim3(256), 0, s, a, units);
+            else hipLaunchKernelGGL((k_attention<false, 1, true>), grid, dim3(256), 0, s, a, units);
+        }
+    } else if (qs == 2) {
         if (wide) hipLaunchKernelGGL((k_attention<true, 2>), grid, dim3(256), 0, s, a, units);
         else hipLaunchKernelGGL((k_attention<false, 2>), grid, dim3(256), 0, s, a, units);
     } else {

@@ -247,11 +247,13 @@ class Hip:
         return self._lib.scunet_hip_name(self._h).decode()
 
     # -- arithmetic mode (no counterpart in the reference) --
-    PRECISIONS = {"fp32": 0, "fp16": 1}
+    PRECISIONS = {"fp32": 0, "fp16": 1, "fp32_mfma": 2}
 
     def set_precision(self, mode):
-        """"fp32" (the reference's arithmetic, the default) or "fp16" (fp16 MFMA operands,
-        fp32 accumulation and planes)."""
+        """"fp32" (the reference's arithmetic to fp32 rounding, the default: split-operand
+        products on the bf16 matrix cores where a kernel has them), "fp32_mfma" (every
+        product on the fp32 matrix cores) or "fp16" (fp16 MFMA operands, fp32 accumulation
+        and planes)."""
         self._check(self._lib.scunet_hip_set_precision(self._h, self.PRECISIONS[mode]))
 
     def precision(self):
