@@ -2713,10 +2713,11 @@ void winograd_filter_slices(const float* u, int cout, int cin, float* u8) {
 // 681-683). The per-head 15x15 bias tables sit in LDS; each lane reads the entries its 64
 // logits use where the logits are formed. V is read transposed straight from memory (4-byte
 // loads, 64 contiguous bytes per key), so the only LDS is the 7.2 KB of tables and the
-// kernel fits in 128 VGPRs: four waves per SIMD, 4 096 (window, head) units in flight.
+// kernel fits in 128 VGPRs: four waves per SIMD, 4 096 (window, head) units in flight. The
+// split-operand form (X6) holds K and V in split form, ~165 VGPRs: three waves per SIMD.
 // ---------------------------------------------------------------------------
 template <bool WIDE, int QS, bool X6 = false>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(X6 ? 2 : 4, X6 ? 2 : 4))) void k_attention(AttnArgs a, long units) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(X6 ? 3 : 4, X6 ? 3 : 4))) void k_attention(AttnArgs a, long units) {
     // Element offsets: 32-bit (WIDE = false) unless the qkv plane reaches 2^32 elements.
     using U = typename std::conditional<WIDE, unsigned long, unsigned>::type;
     __shared__ float rps[8 * 225];                // log2(e) * rel-pos tables, all heads
@@ -2907,10 +2908,12 @@ bool attention(const AttnArgs& a, hipStream_t s, const char** why) {
     if (a.heads > 8) { *why = "attention: at most 8 heads"; return false; }
     const long wheads = long(a.nwh) * a.nww * a.heads;
     if (wheads == 0) return true;
-    // Two query parts per (window, head) when the (window, head) units alone would not give
-    // the chip two rounds of waves, so that loads, products and stores of different waves
-    // overlap (the key and value rows are then read by both parts, from L2 the second time).
-    const int qs = a.qsplit ? a.qsplit : (wheads <= 4096 ? 2 : 1);
+    // fp32 products: two query parts per (window, head) when the (window, head) units alone
+    // would not give the chip two rounds of waves, so that loads, products and stores of
+    // different waves overlap (the key and value rows are then read by both parts, from L2
+    // the second time). The split-operand form (three waves per SIMD) measured faster
+    // without the split at every level (C = 256: 31.4 -> 28.8 us).
+    const int qs = a.qsplit ? a.qsplit : (!a.split && wheads <= 4096 ? 2 : 1);
     const long units = wheads * qs;
     dim3 grid(unsigned((units + 3) / 4));
     if (a.split) {
