@@ -565,7 +565,10 @@ bool block(scunet_hip* h, const std::string& p, float* x, int H, int Wd, int shi
     float* yt = s.y + t;
     const double mlp_flop = 16.0 * double(P) * t * t;
     // At t <= 64 the MLP runs inside the window kernel, on the window's tokens.
-    const bool mlp_in_msa = t <= 64 && !h->unfused_msa && !h->separate_mlp;
+    // In the split-operand mode the t = 64 MLP runs as its own kernel, whose LDS-staged
+    // weight slices feed 128 rows (inside the window kernel every window reads the weight
+    // planes from L2 again): 572 -> 464 us per level-1 block (attention half + MLP).
+    const bool mlp_in_msa = (t <= 32 || (t == 64 && !(h->x6 && !h->h16))) && !h->unfused_msa && !h->separate_mlp;
     if (t <= 256 && !h->unfused_msa) {
         MsaArgs m;
         m.x = yt; m.ldx = c; m.ln_g = W(h, tp + ".ln1.weight"); m.ln_b = W(h, tp + ".ln1.bias");

@@ -1193,7 +1193,7 @@ __global__ __launch_bounds__(NWV * 64) void k_mlp(MlpArgs a) {
     constexpr int EV = H16 ? 8 : 4;               // elements per 16-byte chunk
     constexpr int W0V = HC * T / EV;              // chunks in a W0 slice (and in a W2 slice)
     constexpr int PV = (2 * NP * W0V) / NTH;      // chunks per thread per slice (W0 then W2)
-    static_assert((2 * NP * W0V) % NTH == 0 && W0V % NTH == 0, "slice must split evenly");
+    static_assert((2 * NP * W0V) % NTH == 0 && (X6 || W0V % NTH == 0), "slice must split evenly");
     static_assert(!H16 || HC % 32 == 0, "fp16 slices are whole 32-wide k blocks");
     using ET = std::conditional_t<X6, __bf16, std::conditional_t<H16, _Float16, float>>;
     // DB: double-buffered slices (one barrier per slice); else one buffer, two barriers.
@@ -1455,6 +1455,13 @@ bool mlp(const MlpArgs& a, hipStream_t s, const char** why) {
         return false;
     }
     const bool h16 = a.h0 != nullptr;
+    if (a.x0 && !h16 && a.t == 64) {
+        // t = 64 (the split mode runs it outside the window kernel): 8 waves of two row tiles
+        // share each double-buffered slice (68 KB of LDS). Measured at level 1 of 1080p:
+        // 248 us with one row tile per wave, 227 us with two, 325 / 264 us on 4 waves.
+        go(k_mlp<64, 2, 32, true, 8, true, true, true>, 256, 512);
+        return true;
+    }
     if (a.x0 && !h16 && (a.t == 128 || a.t == 256)) {
         // Split products: 8 waves of one row tile each share every streamed slice (three
         // planes per matrix). t = 128: double-buffered (129 KB of LDS), the normalised rows
