@@ -1266,10 +1266,42 @@ __global__ __launch_bounds__(NWV * 64) void k_mlp(MlpArgs a) {
     // Slice ch: W0 rows ch HC .. + HC - 1 (all T columns) and W2 columns ch HC .. + HC - 1
     // (all T rows). In fp16 mode both come from the k-permuted copies, whose 32-wide k
     // blocks are whole within a slice.
-    f4 pre[PV];
+    // HALF (split products, one buffer): W0's planes of the next slice are fetched during the
+    // first product and W2's during the second, each stored after the barrier that frees its
+    // region, so the prefetch registers hold one matrix's planes at a time.
+    constexpr bool HALF = X6 && !DB;
+    constexpr int PVH = NP * W0V / NTH;
+    static_assert(!HALF || (NP * W0V) % NTH == 0, "half slice must split evenly");
+    f4 pre[HALF ? PVH : PV];
+    auto gload_half = [&](int ch, int which) {
+#pragma unroll
+        for (int i = 0; i < PVH; ++i) {
+            const int f = tid + i * NTH, p = f / W0V, g = f % W0V;
+            if (which == 0) {
+                const int row = g / (T / 8), c = g % (T / 8);
+                pre[i] = ld4(reinterpret_cast<const float*>(a.x0 + long(p) * 4 * T * T + long(ch * HC + row) * T + c * 8));
+            } else {
+                const int row = g / (HC / 8), c = g % (HC / 8);
+                pre[i] = ld4(reinterpret_cast<const float*>(a.x2 + long(p) * 4 * T * T + long(row) * (4 * T) + ch * HC + c * 8));
+            }
+        }
+    };
+    auto lstore_half = [&](int which) {
+#pragma unroll
+        for (int i = 0; i < PVH; ++i) {
+            const int f = tid + i * NTH, p = f / W0V, g = f % W0V;
+            if (which == 0) {
+                const int row = g / (T / 8), c = g % (T / 8);
+                st4(reinterpret_cast<float*>(lds + p * HC * L0 + row * L0 + c * 8), pre[i]);
+            } else {
+                const int row = g / (HC / 8), c = g % (HC / 8);
+                st4(reinterpret_cast<float*>(lds + NP * HC * L0 + p * T * L2 + row * L2 + c * 8), pre[i]);
+            }
+        }
+    };
     auto gload = [&](int ch) {
 #pragma unroll
-        for (int i = 0; i < PV; ++i) {
+        for (int i = 0; i < (HALF ? 0 : PV); ++i) {
             const int f = tid + i * NTH;
             if constexpr (X6) {
                 const int which = f / (NP * W0V), rem = f % (NP * W0V), p = rem / W0V, g = rem % W0V;
@@ -1295,7 +1327,7 @@ __global__ __launch_bounds__(NWV * 64) void k_mlp(MlpArgs a) {
     auto lstore = [&](int b) {
         ET* base = lds + b * BUF;
 #pragma unroll
-        for (int i = 0; i < PV; ++i) {
+        for (int i = 0; i < (HALF ? 0 : PV); ++i) {
             const int f = tid + i * NTH;
             if constexpr (X6) {
                 const int which = f / (NP * W0V), rem = f % (NP * W0V), p = rem / W0V, g = rem % W0V;
@@ -1323,12 +1355,23 @@ __global__ __launch_bounds__(NWV * 64) void k_mlp(MlpArgs a) {
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) acc2[mt][nt] = f4{0.f, 0.f, 0.f, 0.f};
 
-    gload(0);
-    lstore(0);
+    if constexpr (HALF) {
+        gload_half(0, 0);
+        lstore_half(0);
+        gload_half(0, 1);
+        lstore_half(1);
+    } else {
+        gload(0);
+        lstore(0);
+    }
     __syncthreads();
     for (int ch = 0; ch < NCH; ++ch) {
         const ET* cur = lds + (DB ? (ch & 1) * BUF : 0);
-        if (ch + 1 < NCH) gload(ch + 1);
+        if constexpr (HALF) {
+            if (ch + 1 < NCH) gload_half(ch + 1, 0);
+        } else {
+            if (ch + 1 < NCH) gload(ch + 1);
+        }
         f4 acc1[HT][MT];
 #pragma unroll
         for (int ht = 0; ht < HT; ++ht)
@@ -1377,6 +1420,13 @@ __global__ __launch_bounds__(NWV * 64) void k_mlp(MlpArgs a) {
 #pragma unroll
                 for (int r = 0; r < 4; ++r) acc1[ht][mt][r] = gelu_lut(gtab, acc1[ht][mt][r] + bb[r]);
         }
+        if constexpr (HALF) {
+            __syncthreads();   // every wave is past the first product: W0's region is free
+            if (ch + 1 < NCH) {
+                lstore_half(0);
+                gload_half(ch + 1, 1);
+            }
+        }
         if constexpr (X6) {
 #pragma unroll
             for (int kb = 0; kb < HT / 2; ++kb)
@@ -1413,7 +1463,10 @@ __global__ __launch_bounds__(NWV * 64) void k_mlp(MlpArgs a) {
                         for (int mt = 0; mt < MT; ++mt) acc2[mt][nt] = mfma4(wv[r], acc1[ht][mt][r], acc2[mt][nt]);
                 }
         }
-        if constexpr (DB) {
+        if constexpr (HALF) {
+            __syncthreads();   // W2's region is free; W0's next planes are visible after this
+            if (ch + 1 < NCH) lstore_half(1);
+        } else if constexpr (DB) {
             if (ch + 1 < NCH) lstore((ch + 1) & 1);
             __syncthreads();
         } else {
@@ -1424,13 +1477,18 @@ __global__ __launch_bounds__(NWV * 64) void k_mlp(MlpArgs a) {
             }
         }
     }
-    // out^T = W2 H^T: each lane holds 4 consecutive output channels of one row.
+    // out^T = W2 H^T: each lane holds 4 consecutive output channels of one row. Without the
+    // kept rows the row offset is formed again here (an opaque copy of the lane index keeps
+    // the compiler from holding the prologue's 64-bit offset, and spilling it, through the loop).
+    int lie = li, wve = wave;
+    if constexpr (!KEEPX) asm volatile("" : "+v"(lie), "+v"(wve));
+    const long row0e = long(blockIdx.x) * (16 * MT * NWV) + wve * 16 * MT;
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
         const f4 bv = ld4(a.b2 + nt * 16 + lg * 4);
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
-            const long row = row0 + mt * 16 + li;
+            const long row = row0e + mt * 16 + lie;
             if (row < a.M) {
                 float* o = a.x + row * a.ldx + nt * 16 + lg * 4;
                 st4(o, (KEEPX ? xr[KEEPX ? mt : 0][KEEPX ? nt : 0] : ld4(o)) + (acc2[mt][nt] + bv));
