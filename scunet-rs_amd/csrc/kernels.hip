@@ -1142,8 +1142,8 @@ bool pconv(const PconvArgs& a, PconvMode mode, hipStream_t s, const char** why) 
         else if (mode == PC_RESID) ok = launch_pconv<64, 1, 4, PC_RESID, false, true, true>(a, s);
         else ok = launch_pconv<64, 1, 4, PC_CHAIN, false, true, true>(a, s);
     } else if (a.x && a.c == 128 && mode != PC_CHAIN) {
-        if (mode == PC_STORE) ok = launch_pconv<128, 1, 4, PC_STORE, false, true, true>(a, s);
-        else ok = launch_pconv<128, 1, 4, PC_RESID, false, true, true>(a, s);
+        if (mode == PC_STORE) ok = launch_pconv<128, 1, 8, PC_STORE, false, true, true>(a, s);
+        else ok = launch_pconv<128, 1, 8, PC_RESID, false, true, true>(a, s);
     } else if (a.h16 && a.c == 64) {
         if (mode == PC_STORE) ok = launch_pconv<64, 1, 4, PC_STORE, false, true>(a, s);
         else if (mode == PC_RESID) ok = launch_pconv<64, 1, 4, PC_RESID, false, true>(a, s);
