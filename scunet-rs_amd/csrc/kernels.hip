@@ -3510,15 +3510,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(T == 32 ? 2
 // ---------------------------------------------------------------------------
 template <int T, bool MLP, bool H16, bool X6 = false>
 __global__ __launch_bounds__(T * 2) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_wmsa(MsaArgs a, long nw) {
-    // X6: split-operand products (fp32 LDS rows as in the fp32 path, split where loaded).
-    static_assert(!(X6 && H16), "the split products keep fp32 rows");
+    // X6: split-operand products. The normalised tokens are split once, by the wave that
+    // normalises them, into three bf16 planes of k-permuted rows (pitch PH); after the q/k/v
+    // products have read them, the same region takes the head outputs, split by the wave
+    // that forms them. (Without the MLP option: the split mode runs the t = 64 MLP as k_mlp.)
+    static_assert(!(X6 && (H16 || MLP)), "split products: fp32 rows, no fused MLP");
     constexpr int HEADS = T / 32, KG = T / 16, LDX = T + 8;
     // fp16 mode keeps the normalised tokens and the head outputs as k-permuted halves,
     // rows of PH = T + 16 (conflict-free 128-bit reads), inside the same arrays.
     constexpr int PH = T + 16;
     static_assert(PH <= 2 * LDX, "fp16 rows fit the fp32 rows");
-    __shared__ __align__(16) float xs[64 * LDX];   // normalised tokens [token][channel]
-    __shared__ __align__(16) float os[64 * LDX];   // head outputs [token][head * 32 + dim]
+    constexpr int XPS = 64 * PH;   // X6: one plane of the split rows
+    __shared__ __align__(16) float lds[X6 ? 3 * XPS / 2 : 2 * 64 * LDX];
+    float* const xs = lds;                  // normalised tokens [token][channel]
+    float* const os = lds + 64 * LDX;       // head outputs [token][head * 32 + dim]
+    __bf16* const sx = reinterpret_cast<__bf16*>(lds);
     __shared__ __align__(16) float gtab[MLP ? GELU_TABLE : 4];
     _Float16* const xsh = reinterpret_cast<_Float16*>(xs);
     _Float16* const osh = reinterpret_cast<_Float16*>(os);
@@ -3567,7 +3573,16 @@ __global__ __launch_bounds__(T * 2) __attribute__((amdgpu_waves_per_eu(2, 2))) v
             f4 gg = ld4(a.ln_g + kg * 16 + lg * 4), bb = ld4(a.ln_b + kg * 16 + lg * 4);
             v[kg] = (v[kg] - mu) * rs * gg + bb;
         }
-        if constexpr (H16) {
+        if constexpr (X6) {
+#pragma unroll
+            for (int kk = 0; kk < KG / 2; ++kk) {
+                const x8 p = split8(v[2 * kk], v[2 * kk + 1]);
+                __bf16* d = sx + (m * 16 + li) * PH + kk * 32 + lg * 8;
+                stb8(d, p.h);
+                stb8(d + XPS, p.m);
+                stb8(d + 2 * XPS, p.l);
+            }
+        } else if constexpr (H16) {
 #pragma unroll
             for (int kk = 0; kk < KG / 2; ++kk)
                 sth8(xsh + (m * 16 + li) * PH + kk * 32 + lg * 8, pack8(v[2 * kk], v[2 * kk + 1]));
@@ -3595,10 +3610,7 @@ __global__ __launch_bounds__(T * 2) __attribute__((amdgpu_waves_per_eu(2, 2))) v
             for (int kk = 0; kk < KG / 2; ++kk) {
                 x8 xb[4];
 #pragma unroll
-                for (int mt = 0; mt < 4; ++mt) {
-                    const float* r = xs + (mt * 16 + li) * LDX + kk * 32 + lg * 4;
-                    xb[mt] = split8(ld4(r), ld4(r + 16));
-                }
+                for (int mt = 0; mt < 4; ++mt) xb[mt] = ldx8(sx + (mt * 16 + li) * PH + kk * 32 + lg * 8, XPS);
 #pragma unroll
                 for (int d = 0; d < 2; ++d) {
                     const x8 fq = ldx8(wq + (d * 16 + li) * T + kk * 32 + lg * 8, PS);
@@ -3673,6 +3685,8 @@ __global__ __launch_bounds__(T * 2) __attribute__((amdgpu_waves_per_eu(2, 2))) v
                 vf[mt][d] += bv;
             }
         }
+        // X6: every wave has read the split rows; the region now takes the head outputs.
+        if constexpr (X6) __syncthreads();
         const bool row_edge = a.shift > 0 && wh == a.nwh - 1;
         const bool col_edge = a.shift > 0 && ww == a.nww - 1;
         const float SENT = -3.4028234663852886e38f / 4.0f;
@@ -3758,8 +3772,12 @@ __global__ __launch_bounds__(T * 2) __attribute__((amdgpu_waves_per_eu(2, 2))) v
                 }
                 O[0] = O[0] * inv;
                 O[1] = O[1] * inv;
-#pragma unroll
-                for (int nd = 0; nd < 2; ++nd) st4(os + (nt * 16 + li) * LDX + h * 32 + nd * 16 + lg * 4, O[nd]);
+                // The head's dims are k block h of the projection.
+                const x8 p = split8(O[0], O[1]);
+                __bf16* d = sx + (nt * 16 + li) * PH + h * 32 + lg * 8;
+                stb8(d, p.h);
+                stb8(d + XPS, p.m);
+                stb8(d + 2 * XPS, p.l);
             } else if constexpr (H16) {
 #pragma unroll
                 for (int kk = 0; kk < 2; ++kk) {
@@ -3799,10 +3817,7 @@ __global__ __launch_bounds__(T * 2) __attribute__((amdgpu_waves_per_eu(2, 2))) v
         for (int kk = 0; kk < KG / 2; ++kk) {
             x8 ob[4];
 #pragma unroll
-            for (int mt = 0; mt < 4; ++mt) {
-                const float* r = os + (mt * 16 + li) * LDX + kk * 32 + lg * 4;
-                ob[mt] = split8(ld4(r), ld4(r + 16));
-            }
+            for (int mt = 0; mt < 4; ++mt) ob[mt] = ldx8(sx + (mt * 16 + li) * PH + kk * 32 + lg * 8, XPS);
 #pragma unroll
             for (int ct = 0; ct < 2; ++ct) {
                 const x8 fw = ldx8(a.xp + long(c0 + ct * 16 + li) * T + kk * 32 + lg * 8, long(T) * T);
@@ -4005,8 +4020,10 @@ static bool launch_msa(const MsaArgs& a, long nw, hipStream_t s, const char** wh
     if (!H16 && a.xqkv && a.xp && (!a.w0 || (a.x0 && a.x2))) {
         if (a.t == 32 && a.w0) hipLaunchKernelGGL((k_msa<32, true, false, true>), grid, block, 0, s, a, nw);
         else if (a.t == 32) hipLaunchKernelGGL((k_msa<32, false, false, true>), grid, block, 0, s, a, nw);
-        else if (a.t == 64 && a.w0) hipLaunchKernelGGL((k_wmsa<64, true, false, true>), wgrid, wblock, 0, s, a, nw);
-        else if (a.t == 64) hipLaunchKernelGGL((k_wmsa<64, false, false, true>), wgrid, wblock, 0, s, a, nw);
+        else if (a.w0) {
+            *why = "msa_fused: the split-operand form runs the MLP at t >= 64 as its own kernel";
+            return false;
+        } else if (a.t == 64) hipLaunchKernelGGL((k_wmsa<64, false, false, true>), wgrid, wblock, 0, s, a, nw);
         else if (a.t == 128) hipLaunchKernelGGL((k_wmsa<128, false, false, true>), wgrid, wblock, 0, s, a, nw);
         else if (a.t == 256) hipLaunchKernelGGL((k_wmsa<256, false, false, true>), wgrid, wblock, 0, s, a, nw);
         else {
