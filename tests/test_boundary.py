@@ -31,6 +31,16 @@ def test_header_and_python_binding_agree():
     assert sorted(EXPORTS) == declared_symbols()
 
 
+def test_precision_modes_match_the_header():
+    """The arithmetic modes the Python mirror names are the header's #defines."""
+    from scunet_hip import Hip
+    text = open(os.path.join(REPO, "include", "scunet_hip.h")).read()
+    defined = {m.group(1).lower(): int(m.group(2))
+               for m in re.finditer(r"#define SCUNET_HIP_(FP\w+)\s+(\d+)", text)}
+    assert defined == {"fp32": 0, "fp16": 1, "fp32_mfma": 2}
+    assert Hip.PRECISIONS == defined
+
+
 def test_library_exports_every_declared_symbol():
     from scunet_hip import LIB_PATH
     if not os.path.exists(LIB_PATH):
