@@ -40,7 +40,9 @@ WINOGRAD_EXECUTED = 8.0 / 18.0
 # The default fp32 mode forms these classes' products from an exact three-way bf16 split of
 # both fp32 operands: six bf16 part products per fp32 multiply-add on the bf16 matrix cores
 # (fp32 accumulation). Their executed work is 6x the algorithmic FLOP, against the bf16 peak.
-SPLIT_CLASSES = {"conv1x1", "conv1x1_chain", "mlp_fused", "msa_fused", "tblock_fused", "up2x2", "down2x2"}
+# conv3x3_split is the Winograd 3x3 at cin = cout = 32 (level 0) in that form: 6 x 8/18.
+SPLIT_CLASSES = {"conv1x1", "conv1x1_chain", "mlp_fused", "msa_fused", "tblock_fused", "up2x2", "down2x2",
+                 "conv3x3_split"}
 SPLIT_EXECUTED = 6.0
 PRODUCTS = ("fp32 operands, planes and accumulation; the products of the split classes (" +
             ", ".join(sorted(SPLIT_CLASSES)) + ") on the bf16 matrix cores from an exact three-way bf16 split "
@@ -83,16 +85,17 @@ def class_table(rows, steps, peak_tflops, winograd, split=frozenset()):
         agg[3] += byts
     out = []
     for base, (n, ms, flop, byts) in sorted(classes.items(), key=lambda kv: -kv[1][1]):
-        ex = WINOGRAD_EXECUTED if (winograd and base == "conv3x3") else 1.0
+        wino = (winograd and base == "conv3x3") or base == "conv3x3_split"
+        ex = WINOGRAD_EXECUTED if wino else 1.0
         pk = peak_tflops
         if base in split:
-            ex, pk = SPLIT_EXECUTED, PEAK_BF16_TFLOPS
+            ex, pk = ex * SPLIT_EXECUTED, PEAK_BF16_TFLOPS
         k = roofline_of(base, n, ms, flop, byts, pk, ex)
         k["share"] = round(ms / total_ms, 4)
         if base in split:
             k["products"] = "split bf16 x6: achieved/frac count the six bf16 part products per fp32 multiply-add"
             k["fp32_equiv_tflops"] = round(flop / (ms * 1e-3) / 1e12, 3)
-        if ex != 1.0:
+        if wino:
             k["algorithm"] = ("winograd F(2x2,3x3): achieved/frac count the 8*cin*cout FLOP per pixel the MFMA "
                               "units execute; direct_equiv_tflops counts the direct convolution's 18*cin*cout")
             k["direct_equiv_tflops"] = round(flop / (ms * 1e-3) / 1e12, 3)

@@ -427,26 +427,37 @@ bool run_gemm(scunet_hip* h, const char* cls, const GemmArgs& g, GemmA a, GemmE 
 // form's (18 cin cout per pixel), so both paths report comparable rates.
 bool run_conv3(scunet_hip* h, const std::string& name, Conv3Args c, bool relu) {
     long P = long(c.H) * c.W;
-    Span sp(h, "conv3x3", 18.0 * double(P) * c.cin * c.cout,
-            4.0 * (double(P) * (c.cin + c.cout * (relu ? 1 : 2)) + 9.0 * c.cin * c.cout));
     const char* why = nullptr;
     const float* u = W(h, "@wino:" + name + ".weight");
     const half_t* w16 = W16(h, name + ".weight");
-    if (w16 && c.cin == c.cout && (c.cin == 32 || c.cin == 64 || c.cin == 128 || c.cin == 256)) {
+    const bool h16 = w16 && c.cin == c.cout && (c.cin == 32 || c.cin == 64 || c.cin == 128 || c.cin == 256);
+    const bool wino = !h16 && !h->direct3x3 && u && c.cin % 16 == 0 && c.cout % 16 == 0 && c.H % 2 == 0 &&
+                      c.W % 2 == 0;
+    if (h16) {
         c.w16 = w16;
-        if (!conv3x3_h16(c, relu, h->stream, &why)) return fail(h, why);
-    } else if (!h->direct3x3 && u && c.cin % 16 == 0 && c.cout % 16 == 0 && c.H % 2 == 0 && c.W % 2 == 0) {
+    } else if (wino) {
         c.w = u;
         c.w8 = W(h, "@wino8:" + name + ".weight");
         c.cblock = h->wino16 ? 16 : 0;
         c.pair = h->wino_pair ? 1 : 0;
         c.wino3 = h->wino2 ? 0 : h->wino3_all ? 2 : 1;
-        if (!conv3x3_winograd(c, relu, h->stream, &why)) return fail(h, why);
+        c.split = h->x6 && !h->h16 && !h->wino2 ? 1 : 0;
     } else {
         c.w = W(h, name + ".weight");
+    }
+    // The split-operand form is its own profile class (its products run on the bf16 matrix
+    // cores, the other Winograd kernels' on the fp32 ones).
+    const char* cls = wino && conv3x3_winograd_split(c) ? "conv3x3_split" : "conv3x3";
+    Span sp(h, cls, 18.0 * double(P) * c.cin * c.cout,
+            4.0 * (double(P) * (c.cin + c.cout * (relu ? 1 : 2)) + 9.0 * c.cin * c.cout));
+    if (h16) {
+        if (!conv3x3_h16(c, relu, h->stream, &why)) return fail(h, why);
+    } else if (wino) {
+        if (!conv3x3_winograd(c, relu, h->stream, &why)) return fail(h, why);
+    } else {
         if (!conv3x3(c, relu, h->stream, &why)) return fail(h, why);
     }
-    return launched(h, "conv3x3");
+    return launched(h, cls);
 }
 
 // Scratch of one ConvTransBlock at width t on P pixels: y [P][2t], s1 [P][t],

@@ -159,12 +159,15 @@ struct Conv3Args {
     const float* w8 = nullptr;     // Winograd: U as [cin / 8][16][cout][8] (k_wino3; null: not used)
     int wino3 = 1;                 // Winograd: 1 k_wino3 at >= 64 channels; 0 the 32-bit-offset forms
                                    // where the plane allows; 2 k_wino3 everywhere
+    int split = 0;                 // Winograd at cin = cout = 32: split-operand products (k_wino6)
 };
 // relu=true: out = relu(conv); relu=false: out += conv (the conv half's residual).
 bool conv3x3(const Conv3Args& a, bool relu, hipStream_t s, const char** why);
 // The same convolution by Winograd F(2x2, 3x3); a.w is the transformed filter
 // U = G g G^T laid out [16][cout][cin] (see winograd_filter). cin, cout multiples of 16.
 bool conv3x3_winograd(const Conv3Args& a, bool relu, hipStream_t s, const char** why);
+// Whether conv3x3_winograd runs `a` with split-operand products (k_wino6).
+bool conv3x3_winograd_split(const Conv3Args& a);
 // The fp16-operand direct convolution, cin = cout in {32, 64, 128, 256}; a.w16 holds the
 // filters [9][cout][cin] k-permuted (a.w is not read).
 bool conv3x3_h16(const Conv3Args& a, bool relu, hipStream_t s, const char** why);

@@ -2189,6 +2189,242 @@ __global__ __launch_bounds__(512) void k_wino2(Conv3Args a, long tiles, long uni
 }
 
 // ---------------------------------------------------------------------------
+// Winograd F(2x2, 3x3) at cin = cout = 32 with split-operand products (the default fp32
+// mode's form of level 0's 3x3). A unit is a 16 x 16-pixel tile x all 32 output channels,
+// 8 waves: wave pair p owns tile rows 2p, 2p + 1 (16 tiles, lane li = tile) and within the
+// pair wave half hh owns rows 2hh, 2hh + 1 of the transformed 4x4 positions for both
+// 16-channel blocks, so each V is formed and split once. With K = cin = 32 one split product
+// covers a position's whole reduction.
+//   - U = G g G^T, split into three bf16 planes, stays in LDS for the workgroup's lifetime:
+//     rows [16 xi][32 co] of 32 ci (96 KB), 16-byte chunks XOR-swizzled by bit 3 of the row,
+//     so that a half-wave's 16 rows x 2 chunks fall on distinct 16-byte slots mod 32;
+//   - the unit's 18 x 18 x 32 fp32 halo sits in one LDS buffer with a pixel pitch of 9 and a
+//     row pitch of 24 x 9 slots: the 8 tile columns of a half-wave (2 pixels apart) and its
+//     two tile rows (2 pixel rows apart, 16 slots mod 32) read distinct slots. The next unit's
+//     halo is loaded into registers during the products;
+//   - per transformed row the wave reads the two patch rows B^T combines (4 columns, the
+//     lane's 8 channels 4 lg .. + 3 and 16 + 4 lg .. + 3: the k order of the products), forms
+//     t = (B^T d)_i, then V = t B for the row's four positions, splits V and multiplies;
+//   - the output transform is linear in the rows: each wave forms the partial 2x2 outputs
+//     of its two rows, and the pair exchanges one channel block each through the halo buffer
+//     (free once every wave has read it), before the next halo is stashed there.
+// ---------------------------------------------------------------------------
+template <bool RELU, bool BATCH>
+__global__ __launch_bounds__(512) void k_wino6(Conv3Args a, long tiles, long units) {
+    constexpr int HW = 18, HP = 24, LDC = 36;           // halo pixels per row, pitches (floats)
+    constexpr int HSZ = HW * HP * LDC;                   // 15 552 floats
+    constexpr int UPL = 16 * 32 * 32;                    // one U plane, bf16 elements
+    constexpr int HV = (HW * HW * 8 + 511) / 512;        // halo float4 per thread
+    static_assert(8 * 1024 <= HSZ, "the exchange fits in the halo buffer");
+    __shared__ __align__(16) float lds[HSZ + 3 * UPL / 2];
+    float* const hs = lds;
+    __bf16* const us = reinterpret_cast<__bf16*>(lds + HSZ);
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int li = lane & 15, lg = lane >> 4, pair = wave >> 1, hh = wave & 1;
+    const int tx = (a.W + 15) >> 4;
+    const int tr = 2 * pair + (li >> 3), tc = li & 7;
+
+    long u = blockIdx.x;
+    if (u >= units) return;
+    // U planes: item (row r = xi * 32 + co, lane group g) holds ci 4g .. + 3 and 16 + 4g .. + 3.
+    for (int f = tid; f < 16 * 32 * 4; f += 512) {
+        const int r = f >> 2, g = f & 3;
+        const float* src = a.w + long(r) * 32;
+        const x8 v = split8(ld4(src + 4 * g), ld4(src + 16 + 4 * g));
+        __bf16* d = us + r * 32 + 8 * (g ^ (((r >> 3) & 1) << 1));
+        stb8(d, v.h);
+        stb8(d + UPL, v.m);
+        stb8(d + 2 * UPL, v.l);
+    }
+
+    constexpr unsigned NOFF = 0xffffffffu;
+    auto halo_offsets = [&](const WinoUnit& w, unsigned (&ho)[HV]) {
+#pragma unroll
+        for (int i = 0; i < HV; ++i) {
+            const int f = tid + i * 512;
+            const int px = f >> 3, q = f & 7;
+            const int gy = w.y0 - 1 + px / HW, gx = w.x0 - 1 + px % HW;
+            const bool ok = f < HW * HW * 8 && w.y0 >= 0 && gy >= 0 && gy < a.H && gx >= 0 && gx < a.W;
+            ho[i] = ok ? (unsigned(gy) * unsigned(a.W) + unsigned(gx)) * unsigned(a.ldi) + unsigned(q * 4) : NOFF;
+        }
+    };
+    f4 rh[HV];
+    auto load = [&](const unsigned (&ho)[HV]) {
+#pragma unroll
+        for (int i = 0; i < HV; ++i) rh[i] = ho[i] != NOFF ? ld4(a.in + ho[i]) : f4{0.f, 0.f, 0.f, 0.f};
+    };
+    auto stash = [&]() {
+#pragma unroll
+        for (int i = 0; i < HV; ++i) {
+            const int f = tid + i * 512;
+            if (f < HW * HW * 8) {
+                const int px = f >> 3;
+                st4(hs + ((px / HW) * HP + px % HW) * LDC + (f & 7) * 4, rh[i]);
+            }
+        }
+    };
+    // The residual of the accumulate form: this lane's 2 x 2 outputs of channel block hh.
+    auto load_res = [&](const WinoUnit& w, f4 (&res)[2][2]) {
+#pragma unroll
+        for (int a0 = 0; a0 < 2; ++a0)
+#pragma unroll
+            for (int b = 0; b < 2; ++b) {
+                const int y = w.y0 + 2 * tr + a0, x = w.x0 + 2 * tc + b;
+                res[a0][b] = (w.y0 >= 0 && y < a.H && x < a.W)
+                                 ? ld4(a.out + ((unsigned(y) * unsigned(a.W) + unsigned(x)) * unsigned(a.ldo) +
+                                                unsigned(hh * 16 + lg * 4)))
+                                 : f4{0.f, 0.f, 0.f, 0.f};
+            }
+    };
+
+    WinoUnit cur = wino_unit(u, tx, 1, tiles, 32);
+    unsigned hcur[HV], hnxt[HV];
+    halo_offsets(cur, hcur);
+    load(hcur);
+    stash();
+    __syncthreads();   // U and the first halo
+    const float* const base = hs + ((2 * tr) * HP + 2 * tc) * LDC;
+    const __bf16* const ub = us + li * 32 + 8 * (lg ^ ((li >> 3) << 1));
+    // Exchange slots: a wave's 4 partial outputs x 64 lanes, output-major, so that each
+    // 16-byte store or load of the wave covers 1 KB of consecutive LDS.
+    float* const xo = hs + (pair * 2 + (1 - hh)) * 1024 + lane * 4;
+    const float* const xin = hs + (pair * 2 + hh) * 1024 + lane * 4;
+    for (;;) {
+        const long un = u + gridDim.x;
+        const WinoUnit nxt = wino_unit(un < units ? un : u, tx, 1, tiles, 32);
+        if (un < units) {
+            halo_offsets(nxt, hnxt);
+            load(hnxt);
+        }
+        f4 res[2][2];
+        if constexpr (!RELU) load_res(cur, res);
+        // Stacked images: patch row 0 above a tile that starts an image, or row 3 below one
+        // that ends it, reads as zero padding.
+        bool top = false, bot = false;
+        if constexpr (BATCH) {
+            const int yo = cur.y0 + 2 * tr;
+            top = yo % a.img_h == 0;
+            bot = (yo + 2) % a.img_h == 0;
+        }
+        // Partial outputs of this half's rows (channels 16 cb + 4 lg .. + 3): keep[a0][b] for
+        // the wave's own block cb = hh, give[a0][b] for its partner's.
+        // A^T = [1 1 1 0; 0 1 -1 -1]: with r_i[0] = M[i][0] + M[i][1] + M[i][2] and
+        // r_i[1] = M[i][1] - M[i][2] - M[i][3], Y[0][b] = r_0 + r_1 + r_2 and
+        // Y[1][b] = r_1 - r_2 - r_3. Each row is folded in as soon as its products are done.
+        f4 keep[2][2], give[2][2];
+        auto rows = [&](auto HHc) __attribute__((always_inline)) {
+            constexpr int H2 = decltype(HHc)::value;
+#pragma unroll
+            for (int ii = 0; ii < 2; ++ii) {
+                // (B^T d)_i, i = 2 H2 + ii: rows (d0 - d2), (d1 + d2), (d2 - d1), (d1 - d3).
+                constexpr int RA[4] = {0, 1, 2, 1}, RB[4] = {2, 2, 1, 3};
+                const int i = 2 * H2 + ii;
+                f4 t[4][2];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const float* pa = base + (RA[i] * HP + j) * LDC;
+                    const float* pb = base + (RB[i] * HP + j) * LDC;
+                    f4 a0 = ld4(pa + 4 * lg), a1 = ld4(pa + 16 + 4 * lg);
+                    f4 b0 = ld4(pb + 4 * lg), b1 = ld4(pb + 16 + 4 * lg);
+                    if constexpr (BATCH) {
+                        if (i == 0 && top) a0 = a1 = f4{0.f, 0.f, 0.f, 0.f};
+                        if (i == 3 && bot) b0 = b1 = f4{0.f, 0.f, 0.f, 0.f};
+                    }
+                    t[j][0] = i == 1 ? a0 + b0 : a0 - b0;
+                    t[j][1] = i == 1 ? a1 + b1 : a1 - b1;
+                }
+                f4 r[2][2];   // r[cb][b]
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    // (t B)_c: columns (t0 - t2), (t1 + t2), (t2 - t1), (t1 - t3).
+                    f4 v0, v1;
+                    if (c == 0) { v0 = t[0][0] - t[2][0]; v1 = t[0][1] - t[2][1]; }
+                    if (c == 1) { v0 = t[1][0] + t[2][0]; v1 = t[1][1] + t[2][1]; }
+                    if (c == 2) { v0 = t[2][0] - t[1][0]; v1 = t[2][1] - t[1][1]; }
+                    if (c == 3) { v0 = t[1][0] - t[3][0]; v1 = t[1][1] - t[3][1]; }
+                    const x8 xv = split8(v0, v1);
+#pragma unroll
+                    for (int cb = 0; cb < 2; ++cb) {
+                        const f4 m = mfma6(ldx8(ub + ((i * 4 + c) * 32 + cb * 16) * 32, UPL), xv,
+                                           f4{0.f, 0.f, 0.f, 0.f});
+                        if (c == 0) r[cb][0] = m;
+                        if (c == 1) { r[cb][0] += m; r[cb][1] = m; }
+                        if (c == 2) { r[cb][0] += m; r[cb][1] -= m; }
+                        if (c == 3) r[cb][1] -= m;
+                    }
+                }
+#pragma unroll
+                for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+                    for (int b = 0; b < 2; ++b) {
+                        f4 (&yp)[2][2] = cb == H2 ? keep : give;
+                        if (i == 0) yp[0][b] = r[cb][b];
+                        if (i == 1) { yp[0][b] += r[cb][b]; yp[1][b] = r[cb][b]; }
+                        if (i == 2) { yp[0][b] = r[cb][b]; yp[1][b] = f4{0.f, 0.f, 0.f, 0.f} - r[cb][b]; }
+                        if (i == 3) yp[1][b] -= r[cb][b];
+                    }
+            }
+        };
+        if (hh == 0) rows(std::integral_constant<int, 0>{});
+        else rows(std::integral_constant<int, 1>{});
+        __syncthreads();   // every wave is done with this unit's halo: the exchange may use it
+        // This wave finishes channel block hh and hands block 1 - hh to its partner.
+#pragma unroll
+        for (int q = 0; q < 4; ++q) st4(xo + q * 256, give[q >> 1][q & 1]);
+        __syncthreads();
+        f4 got[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) got[q] = ld4(xin + q * 256);
+        __syncthreads();   // the partials are read: the next halo may overwrite them
+        if (un < units) stash();
+        if (cur.y0 >= 0) {
+#pragma unroll
+            for (int a0 = 0; a0 < 2; ++a0)
+#pragma unroll
+                for (int b = 0; b < 2; ++b) {
+                    const int y = cur.y0 + 2 * tr + a0, x = cur.x0 + 2 * tc + b;
+                    if (y >= a.H || x >= a.W) continue;
+                    f4 v = keep[a0][b] + got[a0 * 2 + b];
+                    float* o = a.out + ((unsigned(y) * unsigned(a.W) + unsigned(x)) * unsigned(a.ldo) +
+                                        unsigned(hh * 16 + lg * 4));
+                    if constexpr (RELU) {
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) v[q] = fmaxf(v[q], 0.0f);
+                        st4(o, v);
+                    } else {
+                        st4(o, res[a0][b] + v);
+                    }
+                }
+        }
+        __syncthreads();   // the next unit's halo is visible
+        if (un >= units) break;
+        u = un;
+        cur = nxt;
+#pragma unroll
+        for (int i = 0; i < HV; ++i) hcur[i] = hnxt[i];
+    }
+}
+
+template <bool BATCH>
+static bool launch_wino6(const Conv3Args& a, bool relu, hipStream_t s, const char** why) {
+    static std::atomic<int> cus_c[2] = {}, pc_c[2] = {};
+    Occ oc;
+    if (!query_occ(relu ? k_wino6<true, BATCH> : k_wino6<false, BATCH>, 512, cus_c[relu ? 1 : 0],
+                   pc_c[relu ? 1 : 0], &oc)) {
+        *why = "conv3x3_winograd: device query failed";
+        return false;
+    }
+    const long tiles = long((a.W + 15) / 16) * ((a.H + 15) / 16);
+    const long units = ((tiles + 7) / 8) * 8;
+    const long grid = std::min<long>(units, long(oc.cus) * oc.per_cu);
+    dim3 g{unsigned(grid), 1u, 1u}, block{512u, 1u, 1u};
+    if (relu) hipLaunchKernelGGL((k_wino6<true, BATCH>), g, block, 0, s, a, tiles, units);
+    else hipLaunchKernelGGL((k_wino6<false, BATCH>), g, block, 0, s, a, tiles, units);
+    return true;
+}
+
+// ---------------------------------------------------------------------------
 // Winograd F(2x2, 3x3), the small-footprint form: a unit is 8 x 16 output pixels (4 x 8
 // tiles) x CB output channels (CB = 32 or 64), 4 waves, and the input channels go in
 // slices of 8 whose halo (10 x 18 pixels) and filter part (16 xi x CB x 8) are
@@ -2530,6 +2766,30 @@ static bool launch_wino3(const Conv3Args& a, bool relu, hipStream_t s, const cha
     return true;
 }
 
+// The Winograd kernel a convolution runs on (none: the plane is too large for every form).
+//   - k_wino3 (64-bit unit bases, 32-bit in-unit byte offsets: 10 halo rows of the plane must
+//     span less than 2^31 bytes; stacked images in units of 8 rows) at 64 or more output
+//     channels, where it is the fastest form, and with 32-channel units for planes past
+//     2^32 elements;
+//   - k_wino6 (split-operand products) at cin = cout = 32 when the arguments ask for them;
+//   - k_wino2 / k_wino (32-bit element offsets) elsewhere.
+enum class WinoForm { k3_64, k3_32, split32, other, none };
+static WinoForm wino_form(const Conv3Args& a, bool batch) {
+    const bool fits32 = double(a.H) * a.W * a.ldi < 4294967296.0 && double(a.H) * a.W * a.ldo < 4294967296.0 &&
+                        double(a.cout) * a.cin * 16 < 4294967296.0;
+    const bool k3 = a.w8 && a.cblock == 0 && a.cin % 8 == 0 && a.cout % 32 == 0 &&
+                    10.0 * a.W * a.ldi * 4 < 2147483648.0 && (!batch || a.img_h % 8 == 0);
+    if (k3 && a.wino3 && ((a.cin >= 64 && a.cout % 64 == 0) || a.wino3 == 2))
+        return a.cout % 64 == 0 ? WinoForm::k3_64 : WinoForm::k3_32;
+    if (!fits32) return !k3 ? WinoForm::none : a.cout % 64 == 0 ? WinoForm::k3_64 : WinoForm::k3_32;
+    const bool ures = a.cout == 32 && a.cin == 32 && a.cblock != 16;
+    return ures && a.split ? WinoForm::split32 : WinoForm::other;
+}
+
+bool conv3x3_winograd_split(const Conv3Args& a) {
+    return wino_form(a, a.img_h > 0 && a.img_h < a.H) == WinoForm::split32;
+}
+
 bool conv3x3_winograd(const Conv3Args& a, bool relu, hipStream_t s, const char** why) {
     if (a.cin % 16 != 0 || a.cout % 16 != 0 || (a.H & 1) || (a.W & 1)) {
         *why = "conv3x3_winograd: cin and cout must be multiples of 16 and the plane even";
@@ -2540,25 +2800,18 @@ bool conv3x3_winograd(const Conv3Args& a, bool relu, hipStream_t s, const char**
         *why = "conv3x3_winograd: stacked images must have an even height that divides the plane";
         return false;
     }
-    // k_wino3 (64-bit unit bases, 32-bit in-unit byte offsets: 10 halo rows of the plane must
-    // span less than 2^31 bytes; stacked images in units of 8 rows) at 64 or more output
-    // channels, where it is the fastest form; k_wino2 / k_wino (32-bit element offsets)
-    // elsewhere, and k_wino3 with 32-channel units for planes past 2^32 elements.
-    const bool fits32 = double(a.H) * a.W * a.ldi < 4294967296.0 && double(a.H) * a.W * a.ldo < 4294967296.0 &&
-                        double(a.cout) * a.cin * 16 < 4294967296.0;
-    const bool k3 = a.w8 && a.cblock == 0 && a.cin % 8 == 0 && a.cout % 32 == 0 &&
-                    10.0 * a.W * a.ldi * 4 < 2147483648.0 && (!batch || a.img_h % 8 == 0);
-    if (k3 && a.wino3 && ((a.cin >= 64 && a.cout % 64 == 0) || a.wino3 == 2)) {
-        if (a.cout % 64 == 0)
-            return batch ? launch_wino3<64, true>(a, relu, s, why) : launch_wino3<64, false>(a, relu, s, why);
+    switch (wino_form(a, batch)) {
+    case WinoForm::k3_64:
+        return batch ? launch_wino3<64, true>(a, relu, s, why) : launch_wino3<64, false>(a, relu, s, why);
+    case WinoForm::k3_32:
         return batch ? launch_wino3<32, true>(a, relu, s, why) : launch_wino3<32, false>(a, relu, s, why);
-    }
-    if (!fits32) {
-        if (k3 && a.cout % 64 == 0)
-            return batch ? launch_wino3<64, true>(a, relu, s, why) : launch_wino3<64, false>(a, relu, s, why);
-        if (k3) return batch ? launch_wino3<32, true>(a, relu, s, why) : launch_wino3<32, false>(a, relu, s, why);
+    case WinoForm::split32:
+        return batch ? launch_wino6<true>(a, relu, s, why) : launch_wino6<false>(a, relu, s, why);
+    case WinoForm::none:
         *why = "conv3x3_winograd: plane too large for 32-bit element offsets";
         return false;
+    case WinoForm::other:
+        break;
     }
     // 32 output channels per unit, except at cin >= 256 (level 3 of the forward), where the
     // 16-channel kernel measured faster (238 against 247 us per launch at 1080p).
