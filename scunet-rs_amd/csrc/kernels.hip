@@ -554,7 +554,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     };
     auto a_get = [&](long row, int k) -> f4 {
         if (row >= g.M) return f4{0.f, 0.f, 0.f, 0.f};
-        if constexpr (AM == A_ADD2) return ld4(g.A + row * g.lda + k) + ld4(g.A2 + row * g.lda + k);
         if constexpr (AM == A_S2D) {
             const int tap = k / g.cin, ci = k - tap * g.cin;
             const int ow = g.in_w >> 1;
@@ -592,12 +591,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                 st4(reinterpret_cast<float*>(&Bs[(b * NP + p) * BN * LDB + row * LDB + c * EV]), bpre[p * BV + i]);
             }
     };
-    f4 acur[MT][KG], anext[MT][KG];
+    // The skip-sum operand (A_ADD2) keeps its two loads apart until the slice is used, so the
+    // sum does not wait on memory where the loads are issued; its rows past the end read row
+    // M - 1 (their products only reach output rows that are not stored).
+    constexpr int A2N = AM == A_ADD2 ? MT : 1;
+    f4 acur[MT][KG], anext[MT][KG], anext2[A2N][KG];
     auto aload = [&](long m0, int k0, f4 (&dst)[MT][KG]) {
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-            for (int kg = 0; kg < KG; ++kg) dst[mt][kg] = a_get(m0 + mt * 16 + li, k0 + kg * 16 + lg * 4);
+            for (int kg = 0; kg < KG; ++kg) {
+                if constexpr (AM == A_ADD2) {
+                    const long row = m0 + mt * 16 + li < g.M ? m0 + mt * 16 + li : g.M - 1;
+                    const int k = k0 + kg * 16 + lg * 4;
+                    dst[mt][kg] = ld4(g.A + row * g.lda + k);
+                    anext2[mt][kg] = ld4(g.A2 + row * g.lda + k);
+                } else {
+                    dst[mt][kg] = a_get(m0 + mt * 16 + li, k0 + kg * 16 + lg * 4);
+                }
+            }
     };
     f4 acc[MT][NT], res[MT][NT];
 
@@ -608,6 +620,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     decode(t, m0, n0);
     bload(n0, 0);
     aload(m0, 0, acur);
+    if constexpr (AM == A_ADD2) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int kg = 0; kg < KG; ++kg) acur[mt][kg] += anext2[mt][kg];
+    }
     bstore(0);
     __syncthreads();
     int kb = 0;
@@ -683,9 +701,35 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-                for (int kg = 0; kg < KG; ++kg) acur[mt][kg] = anext[mt][kg];
+                for (int kg = 0; kg < KG; ++kg) {
+                    if constexpr (AM == A_ADD2) acur[mt][kg] = anext[mt][kg] + anext2[mt][kg];
+                    else acur[mt][kg] = anext[mt][kg];
+                }
         }
-        // Epilogue: each lane holds 4 consecutive output columns of one row.
+        // Epilogue: each lane holds 4 consecutive output columns of one row. The
+        // depth-to-space form finds its output pixels once per row (a 32-bit division while
+        // the rows fit) and steps (tap, co) through the 16-column blocks (cout is a multiple
+        // of 16, so no block straddles two taps).
+        long d2s_px[MT];
+        int tap = 0, co = 0;
+        if constexpr (EP == E_D2S) {
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+                const long row = m0 + mt * 16 + li;
+                long ii, jj;
+                if (g.M <= 0xffffffffL) {
+                    const unsigned q = unsigned(row) / unsigned(g.in_w);
+                    ii = q;
+                    jj = unsigned(row) - q * unsigned(g.in_w);
+                } else {
+                    ii = row / g.in_w;
+                    jj = row - ii * g.in_w;
+                }
+                d2s_px[mt] = 2 * ii * 2 * g.in_w + 2 * jj;   // output pixel of tap 0
+            }
+            tap = n0 / g.cout;
+            co = n0 - tap * g.cout + lg * 4;
+        }
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
             const int col = n0 + nt * 16 + lg * 4;
@@ -707,10 +751,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                 } else if constexpr (EP == E_RESID) {
                     st4(g.C + row * g.ldc + col, (RPRE ? res[mt][nt] : ld4(g.R + row * g.ldr + col)) + v);
                 } else {
-                    const long ii = row / g.in_w, jj = row - ii * g.in_w;
-                    const int tap = col / g.cout, co = col - tap * g.cout;
-                    const long oy = 2 * ii + (tap >> 1), ox = 2 * jj + (tap & 1);
-                    st4(g.C + (oy * 2 * g.in_w + ox) * g.cout + co, v);
+                    const long px = d2s_px[mt] + (tap >> 1) * 2 * g.in_w + (tap & 1);
+                    st4(g.C + px * g.cout + co, v);
+                }
+            }
+            if constexpr (EP == E_D2S) {
+                co += 16;
+                if (co >= g.cout) {
+                    co -= g.cout;
+                    ++tap;
                 }
             }
         }
@@ -764,7 +813,9 @@ static void launch_gemm3_e(const GemmArgs& g, GemmE e, hipStream_t s) {
         case E_DUAL: launch_gemm3_k<MT, BN, KC, AM, E_DUAL, H16, X6>(g, s); break;
         case E_GELU: launch_gemm3_k<MT, BN, KC, AM, E_GELU, H16, X6>(g, s); break;
         case E_RESID: launch_gemm3_k<MT, BN, KC, AM, E_RESID, H16, X6>(g, s); break;
-        case E_D2S: launch_gemm3_k<MT, BN, KC, AM, E_D2S, H16, X6>(g, s); break;
+        case E_D2S:
+            if constexpr (AM != A_S2D) launch_gemm3_k<MT, BN, KC, AM, E_D2S, H16, X6>(g, s);
+            break;
     }
 }
 
@@ -798,8 +849,10 @@ static void launch_gemm3_x6(const GemmArgs& g, GemmA a, GemmE e, hipStream_t s) 
 }
 
 static bool launch_gemm3(const GemmArgs& g, GemmA a, GemmE e, hipStream_t s) {
-    // k_gemm3 decodes tile indices in 32 bits (at most 2^31 tiles of 16 rows or more).
-    if (g.M / 16 >= (1L << 31)) return false;
+    // k_gemm3 decodes tile indices in 32 bits (at most 2^31 tiles of 16 rows or more). The
+    // patch operand with the depth-to-space epilogue (no layer of the network) is left to
+    // k_gemm2.
+    if (g.M / 16 >= (1L << 31) || (a == A_S2D && e == E_D2S)) return false;
     if (g.WX && a != A_LN && g.K % 32 == 0 && g.N % 64 == 0) {
         // Split products: at least two 16-row tiles per wave, so the three weight planes a
         // wave reads from LDS per k block feed twice as many products (one tile per wave
