@@ -552,6 +552,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         n0 = int(j - q * unsigned(ntn)) * BN;
         m0 = long(mt) < mtiles ? long(mt) * 64 * MT + wave * 16 * MT : g.M;
     };
+    // The patch operand (A_S2D) finds its 2x2 input patch per load. (Patch bases kept per
+    // tile, with the tap per slice, measured slower at level 0 of the forward: 300 against
+    // 270 us, though faster at level 2.)
     auto a_get = [&](long row, int k) -> f4 {
         if (row >= g.M) return f4{0.f, 0.f, 0.f, 0.f};
         if constexpr (AM == A_S2D) {
@@ -627,6 +630,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             for (int kg = 0; kg < KG; ++kg) acur[mt][kg] += anext2[mt][kg];
     }
     bstore(0);
+    // The first tile's rows arrive before the loop: with loads still pending on its entry
+    // edge, every slice would wait for its own prefetch before its products.
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     int kb = 0;
     for (;;) {
@@ -652,11 +658,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                 if (last) {
 #pragma unroll
                     for (int mt = 0; mt < MT; ++mt) {
-                        const long row = m0 + mt * 16 + li;
+                        const long row = m0 + mt * 16 + li < g.M ? m0 + mt * 16 + li : g.M - 1;
 #pragma unroll
-                        for (int nt = 0; nt < NT; ++nt)
-                            res[mt][nt] = row < g.M ? ld4(g.R + row * g.ldr + n0 + nt * 16 + lg * 4)
-                                                    : f4{0.f, 0.f, 0.f, 0.f};
+                        for (int nt = 0; nt < NT; ++nt) res[mt][nt] = ld4(g.R + row * g.ldr + n0 + nt * 16 + lg * 4);
                     }
                 }
             }
@@ -706,7 +710,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                     else acur[mt][kg] = anext[mt][kg];
                 }
         }
-        // Epilogue: each lane holds 4 consecutive output columns of one row. The
+        // Epilogue: each lane holds 4 consecutive output columns of one row. The bias and the
+        // read-ahead residual are added for every row before the row bound is tested: a load
+        // still pending after a skipped branch would make the next tile's slice loop wait on
+        // every slice (the wait analysis is conservative across the loop head). The
         // depth-to-space form finds its output pixels once per row (a 32-bit division while
         // the rows fit) and steps (tap, co) through the 16-column blocks (cout is a multiple
         // of 16, so no block straddles two taps).
@@ -737,8 +744,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt) {
                 const long row = m0 + mt * 16 + li;
-                if (row >= g.M) continue;
                 f4 v = acc[mt][nt] + bv;
+                if constexpr (RPRE) v = res[mt][nt] + v;
+                if (row >= g.M) continue;
                 if constexpr (EP == E_STORE) {
                     st4(g.C + row * g.ldc + col, v);
                 } else if constexpr (EP == E_DUAL) {
@@ -749,7 +757,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                     for (int r = 0; r < 4; ++r) v[r] = gelu_as(v[r]);
                     st4(g.C + row * g.ldc + col, v);
                 } else if constexpr (EP == E_RESID) {
-                    st4(g.C + row * g.ldc + col, (RPRE ? res[mt][nt] : ld4(g.R + row * g.ldr + col)) + v);
+                    st4(g.C + row * g.ldc + col, RPRE ? v : ld4(g.R + row * g.ldr + col) + v);
                 } else {
                     const long px = d2s_px[mt] + (tap >> 1) * 2 * g.in_w + (tap & 1);
                     st4(g.C + px * g.cout + co, v);
