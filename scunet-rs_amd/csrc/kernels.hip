@@ -1019,8 +1019,12 @@ __global__ __launch_bounds__(NW * 64) void k_pconv(PconvArgs a) {
     constexpr int MSTR = NP * C * LDW;   // one matrix (all its planes)
     using WT = std::conditional_t<X6, __bf16, std::conditional_t<H16, _Float16, float>>;
     __shared__ __align__(16) WT Ws[NMAT * MSTR];
+    // The biases sit in LDS too: a global read in the epilogue would make its wait cover the
+    // next group's rows, issued just before.
+    __shared__ __align__(16) float bs[NMAT * C];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int li = lane & 15, lg = lane >> 4;
+    for (int f = tid; f < NMAT * C; f += NW * 64) bs[f] = f < C ? a.b[f] : a.b1[f - C];
 
     if constexpr (X6) {
         // The pre-split planes (already in the k order of the products), 16 bytes at a time.
@@ -1051,13 +1055,16 @@ __global__ __launch_bounds__(NW * 64) void k_pconv(PconvArgs a) {
     const long stride = long(gridDim.x) * NW;
     long gi = long(blockIdx.x) * NW + wave;
 
+    // Loads are issued on every path (rows past the end read row M - 1, whose products only
+    // reach rows that are not stored; the last group re-reads itself as its "next"), so the
+    // count of outstanding memory operations is the same on all paths and the wait for a
+    // group's rows lands after the next group's loads are issued, not before.
     auto load = [&](long g, f4 (&dst)[MT][KG]) {
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
-            const long row = g * 16 * MT + mt * 16 + li;
+            const long r = g * 16 * MT + mt * 16 + li, row = r < a.M ? r : a.M - 1;
 #pragma unroll
-            for (int kg = 0; kg < KG; ++kg)
-                dst[mt][kg] = row < a.M ? ld4(a.A + row * C + kg * 16 + lg * 4) : f4{0.f, 0.f, 0.f, 0.f};
+            for (int kg = 0; kg < KG; ++kg) dst[mt][kg] = ld4(a.A + row * C + kg * 16 + lg * 4);
         }
     };
     auto product = [&](const WT* Wm, const f4 (&x)[MT][KG], f4 (&acc)[MT][NT]) {
@@ -1113,10 +1120,9 @@ __global__ __launch_bounds__(NW * 64) void k_pconv(PconvArgs a) {
         if constexpr (MODE != PC_STORE) {
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt) {
-                const long row = g * 16 * MT + mt * 16 + li;
+                const long r = g * 16 * MT + mt * 16 + li, row = r < a.M ? r : a.M - 1;
 #pragma unroll
-                for (int nt = 0; nt < NT; ++nt)
-                    dst[mt][nt] = row < a.M ? ld4(a.R + row * C + nt * 16 + lg * 4) : f4{0.f, 0.f, 0.f, 0.f};
+                for (int nt = 0; nt < NT; ++nt) dst[mt][nt] = ld4(a.R + row * C + nt * 16 + lg * 4);
             }
         }
     };
@@ -1126,9 +1132,10 @@ __global__ __launch_bounds__(NW * 64) void k_pconv(PconvArgs a) {
     auto body = [&](long g, const f4 (&cur)[MT][KG], f4 (&nxt)[MT][KG], const f4 (&rc)[MT][NT],
                     f4 (&rn)[MT][NT]) {
         if constexpr (!RPRE) rload(g, rn);
-        if (g + stride < groups) {
-            load(g + stride, nxt);
-            if constexpr (RPRE) rload(g + stride, rn);
+        {
+            const long gn = g + stride < groups ? g + stride : g;
+            load(gn, nxt);
+            if constexpr (RPRE) rload(gn, rn);
         }
         // The weights are loop-invariant; an opaque zero offset keeps the compiler from
         // hoisting every LDS weight read out of the loop into registers.
@@ -1139,7 +1146,7 @@ __global__ __launch_bounds__(NW * 64) void k_pconv(PconvArgs a) {
         product(Wg, cur, acc);
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
-            const f4 bv = ld4(a.b + nt * 16 + lg * 4);
+            const f4 bv = ld4(bs + nt * 16 + lg * 4);
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt) {
                 acc[mt][nt] = acc[mt][nt] + bv;
@@ -1153,7 +1160,7 @@ __global__ __launch_bounds__(NW * 64) void k_pconv(PconvArgs a) {
             product(Wg + MSTR, acc, acc2);
 #pragma unroll
             for (int nt = 0; nt < NT; ++nt) {
-                const f4 bv = ld4(a.b1 + nt * 16 + lg * 4);
+                const f4 bv = ld4(bs + C + nt * 16 + lg * 4);
 #pragma unroll
                 for (int mt = 0; mt < MT; ++mt) {
                     const long row = g * 16 * MT + mt * 16 + li;
