@@ -1267,10 +1267,14 @@ __global__ __launch_bounds__(NWV * 64) void k_mlp(MlpArgs a) {
     // DB: double-buffered slices (one barrier per slice); else one buffer, two barriers.
     __shared__ __align__(16) ET lds[(DB ? 2 : 1) * BUF];
     __shared__ __align__(16) float gtab[GELU_TABLE];
+    // The hidden bias sits in LDS: a global read of it inside the slice loop would make its
+    // wait cover the next slice's weights, issued at the top of the loop.
+    __shared__ __align__(16) float b0s[4 * T];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int li = lane & 15, lg = lane >> 4;
     load_gelu_table(gtab, a.gelu, tid, NTH);
+    for (int f = tid; f < 4 * T; f += NTH) b0s[f] = a.b0[f];
     const long row0 = long(blockIdx.x) * (16 * MT * NWV) + wave * 16 * MT;
 
     f4 xa[MT][KG];
@@ -1435,11 +1439,12 @@ __global__ __launch_bounds__(NWV * 64) void k_mlp(MlpArgs a) {
     __syncthreads();
     for (int ch = 0; ch < NCH; ++ch) {
         const ET* cur = lds + (DB ? (ch & 1) * BUF : 0);
-        if constexpr (HALF) {
-            if (ch + 1 < NCH) gload_half(ch + 1, 0);
-        } else {
-            if (ch + 1 < NCH) gload(ch + 1);
-        }
+        // The next slice's weights are fetched on every pass (the last pass fetches its own
+        // slice again and does not store it), so the number of memory operations in flight
+        // does not depend on the path and the waits cover only what they must.
+        const int chn = ch + 1 < NCH ? ch + 1 : ch;
+        if constexpr (HALF) gload_half(chn, 0);
+        else gload(chn);
         f4 acc1[HT][MT];
 #pragma unroll
         for (int ht = 0; ht < HT; ++ht)
@@ -1482,7 +1487,7 @@ __global__ __launch_bounds__(NWV * 64) void k_mlp(MlpArgs a) {
         }
 #pragma unroll
         for (int ht = 0; ht < HT; ++ht) {
-            const f4 bb = ld4(a.b0 + ch * HC + ht * 16 + lg * 4);
+            const f4 bb = ld4(b0s + ch * HC + ht * 16 + lg * 4);
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -1490,10 +1495,8 @@ __global__ __launch_bounds__(NWV * 64) void k_mlp(MlpArgs a) {
         }
         if constexpr (HALF) {
             __syncthreads();   // every wave is past the first product: W0's region is free
-            if (ch + 1 < NCH) {
-                lstore_half(0);
-                gload_half(ch + 1, 1);
-            }
+            if (ch + 1 < NCH) lstore_half(0);
+            gload_half(chn, 1);
         }
         if constexpr (X6) {
 #pragma unroll
