@@ -4442,8 +4442,12 @@ __global__ __launch_bounds__(256) void k_head(const float* __restrict__ x, int c
     // The 4 pixel groups of this wave, software-pipelined: the next group's input taps are
     // requested before the current group's products and stores (and, when accumulating, the
     // current group's output rows before its products).
+    // Every tap is loaded (from a clamped, valid address) and then selected: taps past K,
+    // pixels past P and taps in the zero padding read as 0. With no load under a branch the
+    // wait before a group's products can leave the next group's loads in flight.
     auto gather = [&](int step, f4 (&av)[2]) {
-        const long p = (long(blockIdx.x) * 16 + wave * 4 + step) * 16 + li;
+        const long pr = (long(blockIdx.x) * 16 + wave * 4 + step) * 16 + li;
+        const long p = pr < P ? pr : P - 1;
         const int yy = int(p / W), xx = int(p - long(yy) * W);
         const int b = yy / H, y = yy - b * H;
         const float* xb = x + long(b) * cin * hh * ww;
@@ -4451,15 +4455,13 @@ __global__ __launch_bounds__(256) void k_head(const float* __restrict__ x, int c
         for (int kg = 0; kg < 2; ++kg)
 #pragma unroll
             for (int s = 0; s < 4; ++s) {
-                const int k = kg * 16 + lg * 4 + s;
-                float v = 0.0f;
-                if (k < K && p < P) {
-                    const int ci = k / 9, tap = k - ci * 9;
-                    const int sy = y + tap / 3 - 1, sx = xx + tap % 3 - 1;
-                    if (sy >= 0 && sy < H && sx >= 0 && sx < W)
-                        v = xb[(long(ci) * hh + (sy < hh ? sy : hh - 1)) * ww + (sx < ww ? sx : ww - 1)];
-                }
-                av[kg][s] = v;
+                const int kr = kg * 16 + lg * 4 + s, k = kr < K ? kr : K - 1;
+                const int ci = k / 9, tap = k - ci * 9;
+                const int sy = y + tap / 3 - 1, sx = xx + tap % 3 - 1;
+                const bool ok = kr < K && pr < P && sy >= 0 && sy < H && sx >= 0 && sx < W;
+                const int cy = min(max(sy, 0), hh - 1), cx = min(max(sx, 0), ww - 1);
+                const float v = xb[(long(ci) * hh + cy) * ww + cx];
+                av[kg][s] = ok ? v : 0.0f;
             }
     };
     f4 cur[2], nxt[2];
@@ -4469,9 +4471,10 @@ __global__ __launch_bounds__(256) void k_head(const float* __restrict__ x, int c
         const long p = (long(blockIdx.x) * 16 + wave * 4 + step) * 16 + li;
         float* o = out + p * 64 + lg * 4;
         f4 prev[4];
-        if (add && p < P) {
+        if (add) {
+            const float* oc = out + (p < P ? p : P - 1) * 64 + lg * 4;
 #pragma unroll
-            for (int nt = 0; nt < 4; ++nt) prev[nt] = ld4(o + nt * 16);
+            for (int nt = 0; nt < 4; ++nt) prev[nt] = ld4(oc + nt * 16);
         }
         if (step + 1 < 4) gather(step + 1, nxt);
         f4 acc[4];
