@@ -719,6 +719,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         // of 16, so no block straddles two taps).
         long d2s_px[MT];
         int tap = 0, co = 0;
+        // A residual not read ahead is read for the whole tile before the first store (rows
+        // clamped), so its reads are in flight together.
+        constexpr bool RLATE = EP == E_RESID && !RPRE && AM == A_ROWS;
+        f4 rl[RLATE ? MT : 1][RLATE ? NT : 1];
+        if constexpr (RLATE) {
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+                const long row = m0 + mt * 16 + li < g.M ? m0 + mt * 16 + li : g.M - 1;
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt) rl[mt][nt] = ld4(g.R + row * g.ldr + n0 + nt * 16 + lg * 4);
+            }
+        }
         if constexpr (EP == E_D2S) {
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt) {
@@ -757,7 +769,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                     for (int r = 0; r < 4; ++r) v[r] = gelu_as(v[r]);
                     st4(g.C + row * g.ldc + col, v);
                 } else if constexpr (EP == E_RESID) {
-                    st4(g.C + row * g.ldc + col, RPRE ? v : ld4(g.R + row * g.ldr + col) + v);
+                    st4(g.C + row * g.ldc + col, RPRE ? v : rl[RLATE ? mt : 0][RLATE ? nt : 0] + v);
                 } else {
                     const long px = d2s_px[mt] + (tap >> 1) * 2 * g.in_w + (tap & 1);
                     st4(g.C + px * g.cout + co, v);
