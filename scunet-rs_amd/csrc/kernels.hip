@@ -1566,15 +1566,39 @@ __global__ __launch_bounds__(NWV * 64) void k_mlp(MlpArgs a) {
     int lie = li, wve = wave;
     if constexpr (!KEEPX) asm volatile("" : "+v"(lie), "+v"(wve));
     const long row0e = long(blockIdx.x) * (16 * MT * NWV) + wve * 16 * MT;
+    if constexpr (KEEPX) {
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-        const f4 bv = ld4(a.b2 + nt * 16 + lg * 4);
+        for (int nt = 0; nt < NT; ++nt) {
+            const f4 bv = ld4(a.b2 + nt * 16 + lg * 4);
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-            const long row = row0e + mt * 16 + lie;
-            if (row < a.M) {
-                float* o = a.x + row * a.ldx + nt * 16 + lg * 4;
-                st4(o, (KEEPX ? xr[KEEPX ? mt : 0][KEEPX ? nt : 0] : ld4(o)) + (acc2[mt][nt] + bv));
+            for (int mt = 0; mt < MT; ++mt) {
+                const long row = row0e + mt * 16 + lie;
+                if (row < a.M) st4(a.x + row * a.ldx + nt * 16 + lg * 4, xr[mt][nt] + (acc2[mt][nt] + bv));
+            }
+        }
+    } else {
+        // The residual rows are read again, RG column groups at a time and all before their
+        // stores (rows clamped), so the reads of a group are in flight together.
+        constexpr int RG = NT < 8 ? NT : 8;
+#pragma unroll
+        for (int n0 = 0; n0 < NT; n0 += RG) {
+            f4 bv[RG], rr[MT][RG];
+#pragma unroll
+            for (int j = 0; j < RG; ++j) bv[j] = ld4(a.b2 + (n0 + j) * 16 + lg * 4);
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+                const long r = row0e + mt * 16 + lie, row = r < a.M ? r : a.M - 1;
+#pragma unroll
+                for (int j = 0; j < RG; ++j) rr[mt][j] = ld4(a.x + row * a.ldx + (n0 + j) * 16 + lg * 4);
+            }
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+                const long row = row0e + mt * 16 + lie;
+                if (row < a.M) {
+#pragma unroll
+                    for (int j = 0; j < RG; ++j)
+                        st4(a.x + row * a.ldx + (n0 + j) * 16 + lg * 4, rr[mt][j] + (acc2[mt][n0 + j] + bv[j]));
+                }
             }
         }
     }
