@@ -250,8 +250,9 @@ bool head_conv(const float* x, int cin, int hh, int ww, int H, int W, const floa
 // m_tail (dim -> cout, 3x3, zero pad) from pixel-major [H*W][dim] into NCHW [cout][oh][ow]
 // for the top-left oh x ow corner (oh <= H, ow <= W: the crop is fused).
 // With nimg > 1, in holds nimg stacked H x W planes and out nimg [cout][oh][ow] images.
+// split: the products on the bf16 matrix cores from split operands (k_tail6); else fp32 FMAs.
 bool tail_conv(const float* in, int dim, int H, int W, const float* w, int cout, float* out,
-               int oh, int ow, hipStream_t s, int nimg = 1);
+               int oh, int ow, hipStream_t s, int nimg = 1, bool split = false);
 
 // A streaming copy of n float4 (the counter-calibration kernel).
 void copy_f4(const void* src, void* dst, long n, hipStream_t s);

@@ -4611,9 +4611,116 @@ __global__ __launch_bounds__(256) void k_tail(const float* __restrict__ in, int 
         for (int o = 0; o < COUT; ++o) out[(long(o) * oh + y) * ow + x] = acc[o];
 }
 
+// ---------------------------------------------------------------------------
+// m_tail with split-operand products (the default fp32 mode). For every pixel p of a tile's
+// halo the 9 x COUT partial sums Z[p][tap * COUT + o] = sum_ci in[p][ci] W[o][ci][tap] are one
+// 64 -> 16 MT product on the bf16 matrix cores (weights as the MFMA rows, split once per
+// workgroup; pixel rows split in registers) and go to LDS; each output is then the sum of
+// its nine taps' values at the shifted pixels, out[o][y][x] = sum_tap Z[(y + dy, x + dx)]
+// [tap * COUT + o], taps in (ky, kx) order. Zero padding: halo pixels outside the image read
+// as zero rows, so their Z is zero. Tiles of 16 x 32 output pixels (halo 18 x 34), one output
+// pixel per thread, 8 waves, persistent over the tiles.
+// ---------------------------------------------------------------------------
+template <int COUT>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) void k_tail6(const float* __restrict__ in, int H, int W, const float* __restrict__ w,
+                                               float* __restrict__ out, int oh, int ow, int tiles) {
+    constexpr int DIM = 64, TH = 16, TW = 32, HWD = TW + 2, HP = (TH + 2) * HWD;   // 612 halo pixels
+    constexpr int NJ = 9 * COUT, MT = (NJ + 15) / 16;
+    constexpr int ZP = (NJ + 3) / 4 * 4;            // Z row pitch: the NJ values, 16-byte aligned
+    constexpr int NG = (HP + 15) / 16, GPW = (NG + 7) / 8;
+    __shared__ __align__(16) float zs[HP * ZP];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, li = lane & 15, lg = lane >> 4;
+    // Weight fragments: row j = 16 mt + li (tap j / COUT, output o = j % COUT), k block kb holds
+    // ci 32 kb + 4 lg .. + 3 and 32 kb + 16 + 4 lg .. + 3, the order of the pixel operand.
+    x8 wf[MT][2];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+            const int j = mt * 16 + li;
+            f4 a0, a1;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int c0 = 32 * kb + 4 * lg + e;
+                a0[e] = j < NJ ? w[((j % COUT) * DIM + c0) * 9 + j / COUT] : 0.0f;
+                a1[e] = j < NJ ? w[((j % COUT) * DIM + c0 + 16) * 9 + j / COUT] : 0.0f;
+            }
+            wf[mt][kb] = split8(a0, a1);
+        }
+    const int tx = (W + TW - 1) / TW, tpi = tx * ((H + TH - 1) / TH);
+    for (int t = blockIdx.x; t < tiles; t += gridDim.x) {
+        const int b = t / tpi, r = t - b * tpi;
+        const int y0 = (r / tx) * TH, x0 = (r - (r / tx) * tx) * TW;
+        const float* const inb = in + long(b) * H * W * DIM;
+        // The wave's halo pixel groups, one at a time with the next group's rows in flight:
+        // every row is loaded (clamped address) and selected. (With the rows of all five
+        // groups in registers at once, two workgroups would not fit a CU.)
+        auto loadg = [&](int gi, f4 (&dst)[4]) {
+            const int p = 16 * (wave + 8 * gi) + li;
+            const int gy = y0 - 1 + p / HWD, gx = x0 - 1 + p % HWD;
+            const bool ok = p < HP && gy >= 0 && gy < H && gx >= 0 && gx < W;
+            const int cy = min(max(gy, 0), H - 1), cx = min(max(gx, 0), W - 1);
+            const float* src = inb + (long(cy) * W + cx) * DIM + lg * 4;
+#pragma unroll
+            for (int kg = 0; kg < 4; ++kg) {
+                const f4 v = ld4(src + kg * 16);
+                dst[kg] = ok ? v : f4{0.f, 0.f, 0.f, 0.f};
+            }
+        };
+        f4 xv[2][4];
+        loadg(0, xv[0]);
+#pragma unroll
+        for (int gi = 0; gi < GPW; ++gi) {
+            if (gi + 1 < GPW) loadg(gi + 1, xv[(gi + 1) & 1]);
+            const int g = wave + 8 * gi;
+            if (g < NG) {   // wave-uniform
+                const f4 (&xc)[4] = xv[gi & 1];
+                const x8 p0 = split8(xc[0], xc[1]), p1 = split8(xc[2], xc[3]);
+                const int p = 16 * g + li;
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) {
+                    f4 d = mfma6(wf[mt][0], p0, f4{0.f, 0.f, 0.f, 0.f});
+                    d = mfma6(wf[mt][1], p1, d);
+                    if (p < HP && mt * 16 + lg * 4 < ZP) st4(zs + p * ZP + mt * 16 + lg * 4, d);
+                }
+            }
+        }
+        __syncthreads();
+        const int ly = tid / TW, lx = tid % TW;
+        float acc[COUT];
+#pragma unroll
+        for (int o = 0; o < COUT; ++o) acc[o] = 0.f;
+#pragma unroll
+        for (int tap = 0; tap < 9; ++tap) {
+            const float* z = zs + ((ly + tap / 3) * HWD + lx + tap % 3) * ZP + tap * COUT;
+#pragma unroll
+            for (int o = 0; o < COUT; ++o) acc[o] += z[o];
+        }
+        const int y = y0 + ly, x = x0 + lx;
+        if (y < oh && x < ow) {
+            float* ob = out + long(b) * COUT * oh * ow;
+#pragma unroll
+            for (int o = 0; o < COUT; ++o) ob[(long(o) * oh + y) * ow + x] = acc[o];
+        }
+        __syncthreads();   // the next tile's Z overwrites this one's
+    }
+}
+
 bool tail_conv(const float* in, int dim, int H, int W, const float* w, int cout, float* out, int oh,
-               int ow, hipStream_t s, int nimg) {
+               int ow, hipStream_t s, int nimg, bool split) {
     if (dim != 64 || nimg < 1 || (nimg > 1 && H % 16 != 0)) return false;
+    if (split && (cout == 3 || cout == 1)) {
+        const long t6 = long((W + 31) / 32) * ((H + 15) / 16) * nimg;
+        if (t6 >= (1L << 31)) return false;
+        static std::atomic<int> cus_c[2] = {}, pc_c[2] = {};
+        Occ oc;
+        const int v = cout == 3 ? 1 : 0;
+        if (!query_occ(cout == 3 ? k_tail6<3> : k_tail6<1>, 512, cus_c[v], pc_c[v], &oc)) return false;
+        const unsigned grid = unsigned(std::min<long>(t6, long(oc.cus) * oc.per_cu));
+        if (cout == 3) hipLaunchKernelGGL(k_tail6<3>, dim3(grid), dim3(512), 0, s, in, H, W, w, out, oh, ow, int(t6));
+        else hipLaunchKernelGGL(k_tail6<1>, dim3(grid), dim3(512), 0, s, in, H, W, w, out, oh, ow, int(t6));
+        return true;
+    }
     const unsigned tiles = unsigned(((W + 15) / 16) * ((H + 15) / 16) * nimg);
     if (cout == 3) hipLaunchKernelGGL(k_tail<3>, dim3(tiles), dim3(256), 0, s, in, H, W, w, out, oh, ow);
     else if (cout == 1) hipLaunchKernelGGL(k_tail<1>, dim3(tiles), dim3(256), 0, s, in, H, W, w, out, oh, ow);
