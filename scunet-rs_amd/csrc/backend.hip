@@ -741,8 +741,10 @@ bool walk(scunet_hip* h, const float* x, int hh, int ww, int H, int Wd, float* y
     if (!dump_plane(h, hook, user, "m_tail_in", cur[0], dim, P[0])) return false;
     {
         Span sp(h, "tail", 2.0 * 9 * in_nc * dim * double(P[0]), 4.0 * (in_nc + dim) * double(P[0]));
+        // The split-product tail in the default and fp16 modes (exact to fp32 level); the
+        // fp32-MFMA mode keeps the fp32 FMA form.
         if (!tail_conv(cur[0], dim, H, Wd, W(h, "m_tail.0.weight"), in_nc, y, oh, ow, h->stream, nimg,
-                       h->x6 && !h->h16))
+                       h->x6 || h->h16))
             return fail(h, "m_tail: unsupported width");
         if (!launched(h, "m_tail")) return false;
     }
@@ -1327,7 +1329,7 @@ int scunet_hip_op_probe(scunet_hip* h, const char* op, const char* name, const f
         } else if (o == "conv3x3" && n == "m_tail.0") {
             nchw_to_nhwc(dx, xt, int(c_in), P, long(c_in), h->stream);
             if (!tail_conv(xt, int(c_in), int(hh), int(ww), wp, int(c_out), yo, int(hh), int(ww), h->stream, 1,
-                           h->x6 && !h->h16))
+                           h->x6 || h->h16))
                 return fail(h, "m_tail: unsupported width");
             if (!launched(h, "op probe")) return false;
             return to_host(h, out, yo, c_out * size_t(P));
