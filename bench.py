@@ -40,9 +40,10 @@ WINOGRAD_EXECUTED = 8.0 / 18.0
 # The default fp32 mode forms these classes' products from an exact three-way bf16 split of
 # both fp32 operands: six bf16 part products per fp32 multiply-add on the bf16 matrix cores
 # (fp32 accumulation). Their executed work is 6x the algorithmic FLOP, against the bf16 peak.
-# conv3x3_split is the Winograd 3x3 at cin = cout = 32 (level 0) in that form: 6 x 8/18.
+# conv3x3_split is the Winograd 3x3 at cin = cout = 32 (level 0) in that form: 6 x 8/18; the
+# tail forms its products from split operands too.
 SPLIT_CLASSES = {"conv1x1", "conv1x1_chain", "mlp_fused", "msa_fused", "tblock_fused", "up2x2", "down2x2",
-                 "conv3x3_split"}
+                 "conv3x3_split", "tail"}
 SPLIT_EXECUTED = 6.0
 PRODUCTS = ("fp32 operands, planes and accumulation; the products of the split classes (" +
             ", ".join(sorted(SPLIT_CLASSES)) + ") on the bf16 matrix cores from an exact three-way bf16 split "
