@@ -2876,8 +2876,9 @@ static bool launch_wino3(const Conv3Args& a, bool relu, hipStream_t s, const cha
 // The Winograd kernel a convolution runs on (none: the plane is too large for every form).
 //   - k_wino3 (64-bit unit bases, 32-bit in-unit byte offsets: 10 halo rows of the plane must
 //     span less than 2^31 bytes; stacked images in units of 8 rows) at 64 or more output
-//     channels, where it is the fastest form, and with 32-channel units for planes past
-//     2^32 elements;
+//     channels, where it is the fastest form: 64-channel units above 64 input channels,
+//     32-channel units at 64 (level 1: 212 -> 208 us, twice the units at three workgroups
+//     per CU) and for planes past 2^32 elements;
 //   - k_wino6 (split-operand products) at cin = cout = 32 when the arguments ask for them;
 //   - k_wino2 / k_wino (32-bit element offsets) elsewhere.
 enum class WinoForm { k3_64, k3_32, split32, other, none };
@@ -2887,7 +2888,7 @@ static WinoForm wino_form(const Conv3Args& a, bool batch) {
     const bool k3 = a.w8 && a.cblock == 0 && a.cin % 8 == 0 && a.cout % 32 == 0 &&
                     10.0 * a.W * a.ldi * 4 < 2147483648.0 && (!batch || a.img_h % 8 == 0);
     if (k3 && a.wino3 && ((a.cin >= 64 && a.cout % 64 == 0) || a.wino3 == 2))
-        return a.cout % 64 == 0 ? WinoForm::k3_64 : WinoForm::k3_32;
+        return a.cout % 64 == 0 && a.cin > 64 ? WinoForm::k3_64 : WinoForm::k3_32;
     if (!fits32) return !k3 ? WinoForm::none : a.cout % 64 == 0 ? WinoForm::k3_64 : WinoForm::k3_32;
     const bool ures = a.cout == 32 && a.cin == 32 && a.cblock != 16;
     return ures && a.split ? WinoForm::split32 : WinoForm::other;
