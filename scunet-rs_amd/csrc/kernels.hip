@@ -2357,17 +2357,21 @@ __global__ __launch_bounds__(512) void k_wino6(Conv3Args a, long tiles, long uni
         }
     };
     f4 rh[HV];
+    // Every halo element is loaded (pixels outside the plane from offset 0) and zeroed when it
+    // is stashed: with no load under a branch, and no use of the loaded values before the
+    // stash, the waits neither stall the products nor cover the previous unit's stores.
     auto load = [&](const unsigned (&ho)[HV]) {
 #pragma unroll
-        for (int i = 0; i < HV; ++i) rh[i] = ho[i] != NOFF ? ld4(a.in + ho[i]) : f4{0.f, 0.f, 0.f, 0.f};
+        for (int i = 0; i < HV; ++i) rh[i] = ld4(a.in + (ho[i] != NOFF ? ho[i] : 0u));
     };
-    auto stash = [&]() {
+    auto stash = [&](const unsigned (&ho)[HV]) {
 #pragma unroll
         for (int i = 0; i < HV; ++i) {
             const int f = tid + i * 512;
             if (f < HW * HW * 8) {
                 const int px = f >> 3;
-                st4(hs + ((px / HW) * HP + px % HW) * LDC + (f & 7) * 4, rh[i]);
+                st4(hs + ((px / HW) * HP + px % HW) * LDC + (f & 7) * 4,
+                    ho[i] != NOFF ? rh[i] : f4{0.f, 0.f, 0.f, 0.f});
             }
         }
     };
@@ -2377,11 +2381,10 @@ __global__ __launch_bounds__(512) void k_wino6(Conv3Args a, long tiles, long uni
         for (int a0 = 0; a0 < 2; ++a0)
 #pragma unroll
             for (int b = 0; b < 2; ++b) {
-                const int y = w.y0 + 2 * tr + a0, x = w.x0 + 2 * tc + b;
-                res[a0][b] = (w.y0 >= 0 && y < a.H && x < a.W)
-                                 ? ld4(a.out + ((unsigned(y) * unsigned(a.W) + unsigned(x)) * unsigned(a.ldo) +
-                                                unsigned(hh * 16 + lg * 4)))
-                                 : f4{0.f, 0.f, 0.f, 0.f};
+                // Pixels past the plane (not stored) read the last row / column.
+                const int y = min(max(w.y0, 0) + 2 * tr + a0, a.H - 1), x = min(w.x0 + 2 * tc + b, a.W - 1);
+                res[a0][b] = ld4(a.out + ((unsigned(y) * unsigned(a.W) + unsigned(x)) * unsigned(a.ldo) +
+                                          unsigned(hh * 16 + lg * 4)));
             }
     };
 
@@ -2389,7 +2392,7 @@ __global__ __launch_bounds__(512) void k_wino6(Conv3Args a, long tiles, long uni
     unsigned hcur[HV], hnxt[HV];
     halo_offsets(cur, hcur);
     load(hcur);
-    stash();
+    stash(hcur);
     __syncthreads();   // U and the first halo
     const float* const base = hs + ((2 * tr) * HP + 2 * tc) * LDC;
     const __bf16* const ub = us + li * 32 + 8 * (lg ^ ((li >> 3) << 1));
@@ -2484,7 +2487,7 @@ __global__ __launch_bounds__(512) void k_wino6(Conv3Args a, long tiles, long uni
 #pragma unroll
         for (int q = 0; q < 4; ++q) got[q] = ld4(xin + q * 256);
         __syncthreads();   // the partials are read: the next halo may overwrite them
-        if (un < units) stash();
+        if (un < units) stash(hnxt);
         if (cur.y0 >= 0) {
 #pragma unroll
             for (int a0 = 0; a0 < 2; ++a0)
