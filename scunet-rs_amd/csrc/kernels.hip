@@ -57,10 +57,27 @@ struct x8 {
 };
 DEVI f4 mfmab(b8 a, b8 b, f4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0); }
 // Two floats -> their rne bf16 parts packed in one register, and the exact remainders.
+// Default form: each part unpacked by a shift or mask, then subtracted (five instructions a
+// pair). DOT form (three a pair): each remainder is one v_dot2c_f32_bf16, x - h as the dot of
+// the packed parts with (-1, 0) or (0, -1) accumulated onto x; both products are exact and
+// x - h is representable, so the sum is exact, bit-equal to the default form for normal
+// values (denormal inputs may be flushed). The DOT form is used where it measured faster:
+// the level-0 split Winograd and the resident-weight 1x1. In the window, MLP and tile-GEMM
+// kernels it measured slower, with more registers or spills, and they keep the default.
+template <bool DOT = false>
 DEVI unsigned split2(float& x0, float& x1) {
     typedef __bf16 b2 __attribute__((ext_vector_type(2)));
     typedef float fl2 __attribute__((ext_vector_type(2)));
     const b2 p = __builtin_convertvector(fl2{x0, x1}, b2);
+    if (DOT) {
+        // The (-1, 0) pair goes in through an SGPR: the compiler encodes it as the inline
+        // constant -1.0, which this operand does not read as that pair.
+        unsigned c0 = 0x0000bf80u, c1 = 0xbf800000u;
+        asm("" : "+s"(c0), "+s"(c1));
+        x0 = __builtin_amdgcn_fdot2_f32_bf16(p, __builtin_bit_cast(b2, c0), x0, false);
+        x1 = __builtin_amdgcn_fdot2_f32_bf16(p, __builtin_bit_cast(b2, c1), x1, false);
+        return __builtin_bit_cast(unsigned, p);
+    }
     const unsigned u = __builtin_bit_cast(unsigned, p);
     x0 -= __builtin_bit_cast(float, u << 16);
     x1 -= __builtin_bit_cast(float, u & 0xffff0000u);
@@ -72,14 +89,15 @@ DEVI unsigned pack2(float x0, float x1) {
     return __builtin_bit_cast(unsigned, __builtin_convertvector(fl2{x0, x1}, b2));
 }
 // The lane's 8 k values (the f4s of two adjacent k groups, as pack8) in split form.
+template <bool DOT = false>
 DEVI x8 split8(f4 lo, f4 hi) {
     typedef unsigned u4 __attribute__((ext_vector_type(4)));
     float v[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
     u4 H, M, L;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) H[i] = split2(v[2 * i], v[2 * i + 1]);
+    for (int i = 0; i < 4; ++i) H[i] = split2<DOT>(v[2 * i], v[2 * i + 1]);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) M[i] = split2(v[2 * i], v[2 * i + 1]);
+    for (int i = 0; i < 4; ++i) M[i] = split2<DOT>(v[2 * i], v[2 * i + 1]);
 #pragma unroll
     for (int i = 0; i < 4; ++i) L[i] = pack2(v[2 * i], v[2 * i + 1]);
     return x8{__builtin_bit_cast(b8, H), __builtin_bit_cast(b8, M), __builtin_bit_cast(b8, L)};
@@ -1089,7 +1107,7 @@ __global__ __launch_bounds__(NW * 64) void k_pconv(PconvArgs a) {
             for (int kk = 0; kk < KG / 2; ++kk) {
                 x8 xv[MT];
 #pragma unroll
-                for (int mt = 0; mt < MT; ++mt) xv[mt] = split8(x[mt][2 * kk], x[mt][2 * kk + 1]);
+                for (int mt = 0; mt < MT; ++mt) xv[mt] = split8<true>(x[mt][2 * kk], x[mt][2 * kk + 1]);
 #pragma unroll
                 for (int nt = 0; nt < NT; ++nt) {
                     const x8 w = ldx8(Wm + (nt * 16 + li) * LDW + kk * 32 + lg * 8, C * LDW);
@@ -2338,7 +2356,7 @@ __global__ __launch_bounds__(512) void k_wino6(Conv3Args a, long tiles, long uni
     for (int f = tid; f < 16 * 32 * 4; f += 512) {
         const int r = f >> 2, g = f & 3;
         const float* src = a.w + long(r) * 32;
-        const x8 v = split8(ld4(src + 4 * g), ld4(src + 16 + 4 * g));
+        const x8 v = split8<true>(ld4(src + 4 * g), ld4(src + 16 + 4 * g));
         __bf16* d = us + r * 32 + 8 * (g ^ (((r >> 3) & 1) << 1));
         stb8(d, v.h);
         stb8(d + UPL, v.m);
@@ -2453,7 +2471,7 @@ __global__ __launch_bounds__(512) void k_wino6(Conv3Args a, long tiles, long uni
                     if (c == 1) { v0 = t[1][0] + t[2][0]; v1 = t[1][1] + t[2][1]; }
                     if (c == 2) { v0 = t[2][0] - t[1][0]; v1 = t[2][1] - t[1][1]; }
                     if (c == 3) { v0 = t[1][0] - t[3][0]; v1 = t[1][1] - t[3][1]; }
-                    const x8 xv = split8(v0, v1);
+                    const x8 xv = split8<true>(v0, v1);
 #pragma unroll
                     for (int cb = 0; cb < 2; ++cb) {
                         const f4 m = mfma6(ldx8(ub + ((i * 4 + c) * 32 + cb * 16) * 32, UPL), xv,
