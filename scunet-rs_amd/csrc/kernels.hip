@@ -2619,25 +2619,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(CB == 32 ? 
     // Halo f4 number f = tid + 256 i of the 10 x 18 x 8 slice (f < 360): byte offset from the
     // halo origin (y0 - 1, x0 - 1), fixed per thread; per unit it becomes NOFF (past the
     // buffer range: the load returns zeros) where the pixel is outside the image.
+    // These per-thread constants are recomputed for every unit (a few integer instructions,
+    // from an opaque copy of tid so that they are not hoisted back out of the unit loop)
+    // rather than held for the kernel's lifetime: held, they were spilled at CB = 64.
     constexpr int NOFF = int(0x80000000u);
-    int hfix[2], hgy[2], hgx[2];
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int f = tid + 256 * i, px = f >> 1, hf = f & 1;
-        const int hy = px / HC, hx = px - hy * HC;
-        hfix[i] = ((hy * int(a.W) + hx) * int(a.ldi) + hf * 4) * 4;
-        hgy[i] = f < HR * HC * 2 ? hy : -1000000;
-        hgx[i] = hx;
-    }
     auto halo_offsets = [&](const Unit& w, int (&ho)[2]) {
+        int otid = tid;
+        asm volatile("" : "+v"(otid));
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
-            const int gy = w.y0 - 1 + hgy[i], gx = w.x0 - 1 + hgx[i];
+            const int f = otid + 256 * i, px = f >> 1, hf = f & 1;
+            const int hy = px / HC, hx = px - hy * HC;
+            const int hfix = ((hy * int(a.W) + hx) * int(a.ldi) + hf * 4) * 4;
+            const int hgy = f < HR * HC * 2 ? hy : -1000000;
+            const int gy = w.y0 - 1 + hgy, gx = w.x0 - 1 + hx;
             bool ok = w.y0 >= 0 && gy >= 0 && gy < a.H && gx >= 0 && gx < a.W;
             if constexpr (BATCH) {
-                if ((hgy[i] == 0 && w.y0 % a.img_h == 0) || (hgy[i] == HR - 1 && (w.y0 + 8) % a.img_h == 0)) ok = false;
+                if ((hgy == 0 && w.y0 % a.img_h == 0) || (hgy == HR - 1 && (w.y0 + 8) % a.img_h == 0)) ok = false;
             }
-            ho[i] = ok ? hfix[i] : NOFF;
+            ho[i] = ok ? hfix : NOFF;
         }
     };
     // Filter slice: f4 number f = tid + 256 i is row r = f >> 1 = (tid >> 1) + 128 i of the
