@@ -3414,8 +3414,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(T == 32 ? 2
     using ET = std::conditional_t<X6, __bf16, std::conditional_t<H16, _Float16, float>>;
     __shared__ __align__(16) ET xs[XSF + MLPF + (XSF + MLPF == 0 ? 8 : 0)];
     __shared__ __align__(16) float gtab[MLP ? GELU_TABLE : 4];
+    // The hidden bias too: read where each hidden chunk's products end, from global memory
+    // its wait came right after them.
+    __shared__ __align__(16) float b0s[MLP ? HID : 4];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     ET* const wm0 = xs + XSF;
+    if constexpr (MLP)
+        for (int f = threadIdx.x; f < HID; f += 256) b0s[f] = a.b0[f];
     ET* const wm2 = wm0 + NP * HID * P0;
     if constexpr (MLP && X6) {
         load_gelu_table(gtab, a.gelu, threadIdx.x, 256);
@@ -3822,7 +3827,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(T == 32 ? 2
             }
 #pragma unroll
             for (int ht = 0; ht < HT; ++ht) {
-                const f4 bb = ld4(a.b0 + ch * HC + ht * 16 + lg * 4);
+                const f4 bb = ld4(b0s + ch * HC + ht * 16 + lg * 4);
 #pragma unroll
                 for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
