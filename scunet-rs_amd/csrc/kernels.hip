@@ -2420,11 +2420,12 @@ __global__ __launch_bounds__(512) void k_wino6(Conv3Args a, long tiles, long uni
     const float* const xin = hs + (pair * 2 + hh) * 1024 + lane * 4;
     for (;;) {
         const long un = u + gridDim.x;
+        // The next unit's halo is requested on every path (the last unit re-reads its own):
+        // with the loads under a branch, the wait before the first products would have to
+        // assume the path without them and cover them too.
         const WinoUnit nxt = wino_unit(un < units ? un : u, tx, 1, tiles, 32);
-        if (un < units) {
-            halo_offsets(nxt, hnxt);
-            load(hnxt);
-        }
+        halo_offsets(nxt, hnxt);
+        load(hnxt);
         f4 res[2][2];
         if constexpr (!RELU) load_res(cur, res);
         // Stacked images: patch row 0 above a tile that starts an image, or row 3 below one
