@@ -4491,9 +4491,21 @@ __global__ __launch_bounds__(256) void k_head(const float* __restrict__ x, int c
     constexpr int LDW = 36;
     __shared__ float sw[64 * LDW];            // W[co][k], k = ci*9 + tap, zero beyond cin*9
     const int K = cin * 9;
-    for (int i = threadIdx.x; i < 64 * 32; i += 256) {
-        const int co = i >> 5, k = i & 31;
-        sw[co * LDW + k] = k < K ? w[co * K + k] : 0.0f;
+    {
+        // All eight reads of a thread in flight together (clamped k, zero selected at the
+        // store): one at a time, each waited for, they were a chain of L2 round trips at the
+        // start of every workgroup.
+        float wv[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int i = threadIdx.x + 256 * j, co = i >> 5, k = i & 31;
+            wv[j] = w[co * K + (k < K ? k : K - 1)];
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int i = threadIdx.x + 256 * j, co = i >> 5, k = i & 31;
+            sw[co * LDW + k] = k < K ? wv[j] : 0.0f;
+        }
     }
     __syncthreads();
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
