@@ -3420,35 +3420,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(T == 32 ? 2
     __shared__ __align__(16) float b0s[MLP ? HID : 4];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     ET* const wm0 = xs + XSF;
-    if constexpr (MLP)
-        for (int f = threadIdx.x; f < HID; f += 256) b0s[f] = a.b0[f];
     ET* const wm2 = wm0 + NP * HID * P0;
-    if constexpr (MLP && X6) {
-        load_gelu_table(gtab, a.gelu, threadIdx.x, 256);
-        for (int f = threadIdx.x; f < NP * HID * T / 8; f += 256) {
-            const int p = f / (HID * T / 8), g = f % (HID * T / 8), r = g / (T / 8), c = g % (T / 8);
-            stb8(wm0 + p * HID * P0 + r * P0 + c * 8, ldb8(a.x0 + long(p) * HID * T + long(r) * T + c * 8));
-        }
-        for (int f = threadIdx.x; f < NP * T * HID / 8; f += 256) {
-            const int p = f / (HID * T / 8), g = f % (HID * T / 8), r = g / (HID / 8), c = g % (HID / 8);
-            stb8(wm2 + p * T * P2 + r * P2 + c * 8, ldb8(a.x2 + long(p) * HID * T + long(r) * HID + c * 8));
-        }
-    } else if constexpr (MLP) {
-        load_gelu_table(gtab, a.gelu, threadIdx.x, 256);
-        constexpr int EV = H16 ? 8 : 4;   // elements per 16-byte chunk
-        const ET* g0 = H16 ? reinterpret_cast<const ET*>(a.h0) : reinterpret_cast<const ET*>(a.w0);
-        const ET* g2 = H16 ? reinterpret_cast<const ET*>(a.h2) : reinterpret_cast<const ET*>(a.w2);
-        for (int f = threadIdx.x; f < HID * T / EV; f += 256) {
-            const int r = f / (T / EV), c = f % (T / EV);
-            st4(reinterpret_cast<float*>(wm0 + r * P0 + c * EV),
-                ld4(reinterpret_cast<const float*>(g0 + long(r) * T + c * EV)));
-        }
-        for (int f = threadIdx.x; f < T * HID / EV; f += 256) {
-            const int r = f / (HID / EV), c = f % (HID / EV);
-            st4(reinterpret_cast<float*>(wm2 + r * P2 + c * EV),
-                ld4(reinterpret_cast<const float*>(g2 + long(r) * HID + c * EV)));
-        }
-    }
     const int li = lane & 15, lg = lane >> 4;
     const long wi = long(blockIdx.x) * 4 + wave;
     const bool valid = wi < nw;
@@ -3467,18 +3439,85 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(T == 32 ? 2
         if (x >= a.W) x -= a.W;
         return (ybase + y) * a.W + x;
     };
+    // The window's token rows are requested first (invalid waves read window 0's rows and
+    // discard them), so they are in flight with the staging reads below.
+    f4 xin[4][KG];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+        const long row = rowof(mt * 16 + li);
+#pragma unroll
+        for (int kg = 0; kg < KG; ++kg) xin[mt][kg] = ld4(a.x + row * a.ldx + kg * 16 + lg * 4);
+    }
+    f4 ln1g[KG], ln1b[KG];
+#pragma unroll
+    for (int kg = 0; kg < KG; ++kg) {
+        ln1g[kg] = ld4(a.ln_g + kg * 16 + lg * 4);
+        ln1b[kg] = ld4(a.ln_b + kg * 16 + lg * 4);
+    }
+    // The staging of the GELU table, the hidden bias and the MLP weights issues all of a
+    // thread's reads before its LDS stores, so they are in flight together (a load-store
+    // loop waits a full L2 round trip per pass, at the start of every workgroup).
+    f4 gtv = f4{0.f, 0.f, 0.f, 0.f};
+    float b0v = 0.f;
+    if constexpr (MLP) {
+        static_assert(GELU_TABLE / 4 <= 256 && HID <= 256, "one table chunk and one bias per thread");
+        gtv = ld4(a.gelu + 4 * min(int(threadIdx.x), GELU_TABLE / 4 - 1));
+        b0v = a.b0[min(int(threadIdx.x), HID - 1)];
+    }
+    if constexpr (MLP && X6) {
+        constexpr int NV = NP * HID * T / 8 / 256;   // 16-byte chunks per thread, each matrix
+        static_assert(NV * 256 == NP * HID * T / 8, "weight staging must split evenly");
+        b8 v0[NV], v2[NV];
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+            const int f = threadIdx.x + 256 * j;
+            const int p = f / (HID * T / 8), g = f % (HID * T / 8);
+            v0[j] = ldb8(a.x0 + long(p) * HID * T + long(g / (T / 8)) * T + (g % (T / 8)) * 8);
+            v2[j] = ldb8(a.x2 + long(p) * HID * T + long(g / (HID / 8)) * HID + (g % (HID / 8)) * 8);
+        }
+        __builtin_amdgcn_sched_barrier(0);   // every read above, every store below
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+            const int f = threadIdx.x + 256 * j;
+            const int p = f / (HID * T / 8), g = f % (HID * T / 8);
+            stb8(wm0 + p * HID * P0 + (g / (T / 8)) * P0 + (g % (T / 8)) * 8, v0[j]);
+            stb8(wm2 + p * T * P2 + (g / (HID / 8)) * P2 + (g % (HID / 8)) * 8, v2[j]);
+        }
+    } else if constexpr (MLP) {
+        constexpr int EV = H16 ? 8 : 4;   // elements per 16-byte chunk
+        constexpr int NV = HID * T / EV / 256;
+        static_assert(NV * 256 == HID * T / EV, "weight staging must split evenly");
+        const ET* g0 = H16 ? reinterpret_cast<const ET*>(a.h0) : reinterpret_cast<const ET*>(a.w0);
+        const ET* g2 = H16 ? reinterpret_cast<const ET*>(a.h2) : reinterpret_cast<const ET*>(a.w2);
+        f4 v0[NV], v2[NV];
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+            const int f = threadIdx.x + 256 * j;
+            v0[j] = ld4(reinterpret_cast<const float*>(g0 + long(f / (T / EV)) * T + (f % (T / EV)) * EV));
+            v2[j] = ld4(reinterpret_cast<const float*>(g2 + long(f / (HID / EV)) * HID + (f % (HID / EV)) * EV));
+        }
+        __builtin_amdgcn_sched_barrier(0);   // every read above, every store below
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+            const int f = threadIdx.x + 256 * j;
+            st4(reinterpret_cast<float*>(wm0 + (f / (T / EV)) * P0 + (f % (T / EV)) * EV), v0[j]);
+            st4(reinterpret_cast<float*>(wm2 + (f / (HID / EV)) * P2 + (f % (HID / EV)) * EV), v2[j]);
+        }
+    }
+    if constexpr (MLP) {
+        if (threadIdx.x < GELU_TABLE / 4) st4(gtab + 4 * threadIdx.x, gtv);
+        if (threadIdx.x < HID) b0s[threadIdx.x] = b0v;
+    }
 
     // 1. LN1 of the window's tokens into LDS. The raw rows stay in registers for the
     // attention residual (the wave is register-limited to two per SIMD either way).
-    f4 xin[4][KG];
     x8 xbx[X6 ? 4 : 1][X6 ? KG / 2 : 1];
     if (valid) {
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt) {
-            const long row = rowof(mt * 16 + li);
             f4 v[KG];
 #pragma unroll
-            for (int kg = 0; kg < KG; ++kg) xin[mt][kg] = v[kg] = ld4(a.x + row * a.ldx + kg * 16 + lg * 4);
+            for (int kg = 0; kg < KG; ++kg) v[kg] = xin[mt][kg];
             float sm = 0.f;
 #pragma unroll
             for (int kg = 0; kg < KG; ++kg) sm += (v[kg].x + v[kg].y) + (v[kg].z + v[kg].w);
@@ -3496,8 +3535,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(T == 32 ? 2
             const float rs = __builtin_amdgcn_rsqf(q * (1.0f / float(T)) + 1e-5f);
 #pragma unroll
             for (int kg = 0; kg < KG; ++kg) {
-                f4 gg = ld4(a.ln_g + kg * 16 + lg * 4), bb = ld4(a.ln_b + kg * 16 + lg * 4);
-                v[kg] = (v[kg] - mu) * rs * gg + bb;
+                v[kg] = (v[kg] - mu) * rs * ln1g[kg] + ln1b[kg];
             }
             if constexpr (X6) {
 #pragma unroll
