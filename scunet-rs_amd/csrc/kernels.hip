@@ -1303,68 +1303,39 @@ __global__ __launch_bounds__(NWV * 64) void k_mlp(MlpArgs a) {
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int li = lane & 15, lg = lane >> 4;
-    load_gelu_table(gtab, a.gelu, tid, NTH);
-    for (int f = tid; f < 4 * T; f += NTH) b0s[f] = a.b0[f];
+    // The prologue's reads (GELU table, hidden bias, the rows, the LayerNorm parameters and
+    // the first slice's weights, below) are issued as one batch before any of them is used or
+    // stored: one at a time, each waited for, they were a chain of L2 round trips at the start
+    // of every workgroup. Rows past the end read row M - 1 and are replaced by zeros.
+    constexpr int NGT = (GELU_TABLE / 4 + NTH - 1) / NTH, NB0 = (4 * T + NTH - 1) / NTH;
+    f4 gtv[NGT];
+    float b0v[NB0];
+#pragma unroll
+    for (int j = 0; j < NGT; ++j) gtv[j] = ld4(a.gelu + 4 * min(tid + j * NTH, GELU_TABLE / 4 - 1));
+#pragma unroll
+    for (int j = 0; j < NB0; ++j) b0v[j] = a.b0[min(tid + j * NTH, 4 * T - 1)];
     const long row0 = long(blockIdx.x) * (16 * MT * NWV) + wave * 16 * MT;
 
     f4 xa[MT][KG];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
-        const long r = row0 + mt * 16 + li;
-#pragma unroll
-        for (int kg = 0; kg < KG; ++kg)
-            xa[mt][kg] = r < a.M ? ld4(a.x + r * a.ldx + kg * 16 + lg * 4) : f4{0.f, 0.f, 0.f, 0.f};
-    }
-    // The raw rows stay in registers for the residual, unless they would crowd out the
-    // accumulators (then they are read again at the end).
-    constexpr bool KEEPX = KEEP && MT * KG <= 16;
-    f4 xr[KEEPX ? MT : 1][KEEPX ? KG : 1];
-    if constexpr (KEEPX) {
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-            for (int kg = 0; kg < KG; ++kg) xr[mt][kg] = xa[mt][kg];
-    }
-    // LayerNorm, two-pass (cpu.rs:338-357).
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-        float s = 0.f;
-#pragma unroll
-        for (int kg = 0; kg < KG; ++kg) s += (xa[mt][kg].x + xa[mt][kg].y) + (xa[mt][kg].z + xa[mt][kg].w);
-        s += __shfl_xor(s, 16);
-        s += __shfl_xor(s, 32);
-        const float mu = s / float(T);
-        float q = 0.f;
+        const long r = row0 + mt * 16 + li, rc = r < a.M ? r : a.M - 1;
 #pragma unroll
         for (int kg = 0; kg < KG; ++kg) {
-            f4 d = xa[mt][kg] - mu;
-            q += (d.x * d.x + d.y * d.y) + (d.z * d.z + d.w * d.w);
+            const f4 v = ld4(a.x + rc * a.ldx + kg * 16 + lg * 4);
+            xa[mt][kg] = r < a.M ? v : f4{0.f, 0.f, 0.f, 0.f};
         }
-        q += __shfl_xor(q, 16);
-        q += __shfl_xor(q, 32);
-        const float rs = __builtin_amdgcn_rsqf(q * (1.0f / float(T)) + 1e-5f);
+    }
+    // The LayerNorm parameters join the batch while they fit the registers (t <= 128).
+    constexpr bool LNPRE = KG <= 8;
+    f4 lng[LNPRE ? KG : 1], lnb[LNPRE ? KG : 1];
+    if constexpr (LNPRE) {
 #pragma unroll
         for (int kg = 0; kg < KG; ++kg) {
-            f4 g = ld4(a.ln_g + kg * 16 + lg * 4), b = ld4(a.ln_b + kg * 16 + lg * 4);
-            xa[mt][kg] = (xa[mt][kg] - mu) * rs * g + b;
+            lng[kg] = ld4(a.ln_g + kg * 16 + lg * 4);
+            lnb[kg] = ld4(a.ln_b + kg * 16 + lg * 4);
         }
     }
-    // 16-bit operands of the first product (k groups 2kk, 2kk + 1 packed), or their split form.
-    h8 xh[H16 && !X6 ? MT : 1][H16 && !X6 ? KG / 2 : 1];
-    // XS: the normalised rows kept in split form (else split again for every slice).
-    x8 xs[X6 && XS ? MT : 1][X6 && XS ? KG / 2 : 1];
-    if constexpr (X6 && XS) {
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-            for (int kk = 0; kk < KG / 2; ++kk) xs[mt][kk] = split8(xa[mt][2 * kk], xa[mt][2 * kk + 1]);
-    } else if constexpr (H16) {
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-            for (int kk = 0; kk < KG / 2; ++kk) xh[mt][kk] = pack8(xa[mt][2 * kk], xa[mt][2 * kk + 1]);
-    }
-
     // Slice ch: W0 rows ch HC .. + HC - 1 (all T columns) and W2 columns ch HC .. + HC - 1
     // (all T rows). In fp16 mode both come from the k-permuted copies, whose 32-wide k
     // blocks are whole within a slice.
@@ -1457,13 +1428,71 @@ __global__ __launch_bounds__(NWV * 64) void k_mlp(MlpArgs a) {
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) acc2[mt][nt] = f4{0.f, 0.f, 0.f, 0.f};
 
+    if constexpr (HALF) gload_half(0, 0);
+    else gload(0);
+    __builtin_amdgcn_sched_barrier(0);   // every prologue read above, its first use below
+#pragma unroll
+    for (int j = 0; j < NGT; ++j)
+        if (tid + j * NTH < GELU_TABLE / 4) st4(gtab + 4 * (tid + j * NTH), gtv[j]);
+#pragma unroll
+    for (int j = 0; j < NB0; ++j)
+        if (tid + j * NTH < 4 * T) b0s[tid + j * NTH] = b0v[j];
+    // The raw rows stay in registers for the residual, unless they would crowd out the
+    // accumulators (then they are read again at the end).
+    constexpr bool KEEPX = KEEP && MT * KG <= 16;
+    f4 xr[KEEPX ? MT : 1][KEEPX ? KG : 1];
+    if constexpr (KEEPX) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int kg = 0; kg < KG; ++kg) xr[mt][kg] = xa[mt][kg];
+    }
+    // LayerNorm, two-pass (cpu.rs:338-357).
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+        float s = 0.f;
+#pragma unroll
+        for (int kg = 0; kg < KG; ++kg) s += (xa[mt][kg].x + xa[mt][kg].y) + (xa[mt][kg].z + xa[mt][kg].w);
+        s += __shfl_xor(s, 16);
+        s += __shfl_xor(s, 32);
+        const float mu = s / float(T);
+        float q = 0.f;
+#pragma unroll
+        for (int kg = 0; kg < KG; ++kg) {
+            f4 d = xa[mt][kg] - mu;
+            q += (d.x * d.x + d.y * d.y) + (d.z * d.z + d.w * d.w);
+        }
+        q += __shfl_xor(q, 16);
+        q += __shfl_xor(q, 32);
+        const float rs = __builtin_amdgcn_rsqf(q * (1.0f / float(T)) + 1e-5f);
+#pragma unroll
+        for (int kg = 0; kg < KG; ++kg) {
+            const f4 g = LNPRE ? lng[LNPRE ? kg : 0] : ld4(a.ln_g + kg * 16 + lg * 4);
+            const f4 b = LNPRE ? lnb[LNPRE ? kg : 0] : ld4(a.ln_b + kg * 16 + lg * 4);
+            xa[mt][kg] = (xa[mt][kg] - mu) * rs * g + b;
+        }
+    }
+    // 16-bit operands of the first product (k groups 2kk, 2kk + 1 packed), or their split form.
+    h8 xh[H16 && !X6 ? MT : 1][H16 && !X6 ? KG / 2 : 1];
+    // XS: the normalised rows kept in split form (else split again for every slice).
+    x8 xs[X6 && XS ? MT : 1][X6 && XS ? KG / 2 : 1];
+    if constexpr (X6 && XS) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int kk = 0; kk < KG / 2; ++kk) xs[mt][kk] = split8(xa[mt][2 * kk], xa[mt][2 * kk + 1]);
+    } else if constexpr (H16) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int kk = 0; kk < KG / 2; ++kk) xh[mt][kk] = pack8(xa[mt][2 * kk], xa[mt][2 * kk + 1]);
+    }
+
     if constexpr (HALF) {
-        gload_half(0, 0);
         lstore_half(0);
         gload_half(0, 1);
         lstore_half(1);
     } else {
-        gload(0);
         lstore(0);
     }
     __syncthreads();
