@@ -3033,18 +3033,34 @@ __global__ __launch_bounds__(NWV * 64) void k_conv3h(Conv3Args a, int tiles_x, l
 #pragma unroll
     for (int k = 0; k < NA; ++k) wload(k, wa[k]);
 
-    // Stage the halo (zero outside the plane: the convolution's zero padding).
-    constexpr int NSLOT = (R + 2) * RP * SP;
-    for (int f = tid; f < NSLOT; f += NWV * 64) {
-        const int q = f % SP, p = f / SP;
-        const int hr = p / RP, hc = p - hr * RP;
-        const int gy = y0 - 1 + hr, gx = x0 - 1 + hc;
-        h8 v = h8{0, 0, 0, 0, 0, 0, 0, 0};
-        if (gy >= ylo && gy < yhi && gx >= 0 && gx < a.W) {
-            const float* src = a.in + (long(gy) * a.W + gx) * a.ldi + 32 * (q >> 2) + 4 * (q & 3);
-            v = pack8(ld4(src), ld4(src + 16));
+    // Stage the halo (zero outside the plane: the convolution's zero padding), four passes
+    // of the workgroup at a time (two above 32 channels, where the filters hold more
+    // registers): their reads come from clamped addresses and are issued
+    // together, and the zeros are selected at the LDS store (a read under the bounds test
+    // was waited for in its own pass, one L2 round trip each).
+    constexpr int NSLOT = (R + 2) * RP * SP, NTH = NWV * 64, NPASS = (NSLOT + NTH - 1) / NTH, PB = C <= 32 ? 4 : 2;
+#pragma unroll
+    for (int i0 = 0; i0 < NPASS; i0 += PB) {
+        f4 va[PB], vb[PB];
+        bool ok[PB];
+#pragma unroll
+        for (int j = 0; j < PB; ++j) {
+            const int f = tid + (i0 + j) * NTH, fc = f < NSLOT ? f : NSLOT - 1;
+            const int q = fc % SP, p = fc / SP;
+            const int hr = p / RP, hc = p - hr * RP;
+            const int gy = y0 - 1 + hr, gx = x0 - 1 + hc;
+            ok[j] = i0 + j < NPASS && f < NSLOT && gy >= ylo && gy < yhi && gx >= 0 && gx < a.W;
+            const int cy = min(max(gy, ylo), yhi - 1), cx = min(max(gx, 0), a.W - 1);
+            const float* src = a.in + (long(cy) * a.W + cx) * a.ldi + 32 * (q >> 2) + 4 * (q & 3);
+            va[j] = ld4(src);
+            vb[j] = ld4(src + 16);
         }
-        sth8(halo + (p * SPP + q) * 8, v);
+#pragma unroll
+        for (int j = 0; j < PB; ++j) {
+            const int f = tid + (i0 + j) * NTH;
+            if (i0 + j < NPASS && f < NSLOT)
+                sth8(halo + ((f / SP) * SPP + f % SP) * 8, ok[j] ? pack8(va[j], vb[j]) : h8{0, 0, 0, 0, 0, 0, 0, 0});
+        }
     }
     __syncthreads();
 
@@ -3083,6 +3099,18 @@ __global__ __launch_bounds__(NWV * 64) void k_conv3h(Conv3Args a, int tiles_x, l
     // Lanes hold output channels cog*32 + 16j + 4lg .. + 3 of pixel (y0 + r, x0 + 16 strip + li).
     const int x = x0 + strip * 16 + li;
     if (x >= a.W) return;
+    // Accumulate form: the residual reads of all R rows are issued together, from clamped
+    // rows, before the first store (one at a time under the row test, each was waited for).
+    f4 res[RELU ? 1 : R][2];
+    if constexpr (!RELU) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int yc = min(y0 + r, a.H - 1);
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+                res[r][j] = ld4(a.out + (long(yc) * a.W + x) * a.ldo + cog * 32 + j * 16 + lg * 4);
+        }
+    }
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         const int y = y0 + r;
@@ -3094,7 +3122,7 @@ __global__ __launch_bounds__(NWV * 64) void k_conv3h(Conv3Args a, int tiles_x, l
                 const f4 v = acc[r][j];
                 st4(o, f4{fmaxf(v.x, 0.f), fmaxf(v.y, 0.f), fmaxf(v.z, 0.f), fmaxf(v.w, 0.f)});
             } else {
-                st4(o, ld4(o) + acc[r][j]);
+                st4(o, res[r][j] + acc[r][j]);
             }
         }
     }
