@@ -540,6 +540,9 @@ __global__ __launch_bounds__(256) void k_gemm2(GemmArgs g) {
 // double-buffered in LDS; the epilogue uses registers only). Tile t = 8 j + xcd: the
 // N-blocks of one M-tile are consecutive j on one XCD and share its L2.
 // ---------------------------------------------------------------------------
+// Widest N the persistent GEMM serves (its bias is staged in LDS): the 2x2 transposed conv
+// at 256 output channels, N = 4 * 256.
+constexpr int GEMM3_NMAX = 1024;
 template <int MT, int BN, int KC, int AM, int EP, bool H16, bool X6 = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_gemm3(GemmArgs g, long tiles) {
     // fp16 mode: a K slice is one 32-wide k block of the k-permuted weights, staged as halves
@@ -556,6 +559,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     constexpr bool RPRE = EP == E_RESID && MT * NT <= 8;
     using ET = std::conditional_t<X6, __bf16, std::conditional_t<H16, _Float16, float>>;
     __shared__ __align__(16) ET Bs[2 * NP * BN * LDB];
+    // The bias of every column, staged once per (persistent) workgroup: read from global
+    // memory in the epilogue, each column block's read was waited for before its stores,
+    // and that wait also covered the next tile's operands, requested during the last slice.
+    __shared__ __align__(16) float bsh[GEMM3_NMAX];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int li = lane & 15, lg = lane >> 4;
@@ -573,16 +580,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     // The patch operand (A_S2D) finds its 2x2 input patch per load. (Patch bases kept per
     // tile, with the tap per slice, measured slower at level 0 of the forward: 300 against
     // 270 us, though faster at level 2.)
+    // Rows past the end read row M - 1 and are replaced by zeros (no load under a branch).
     auto a_get = [&](long row, int k) -> f4 {
-        if (row >= g.M) return f4{0.f, 0.f, 0.f, 0.f};
+        const long rc = row < g.M ? row : g.M - 1;
+        f4 v;
         if constexpr (AM == A_S2D) {
             const int tap = k / g.cin, ci = k - tap * g.cin;
             const int ow = g.in_w >> 1;
-            const long oy = row / ow, ox = row - oy * ow;
+            const long oy = rc / ow, ox = rc - oy * ow;
             const long ip = (2 * oy + (tap >> 1)) * long(g.in_w) + 2 * ox + (tap & 1);
-            return ld4(g.A + ip * g.cin + ci);
+            v = ld4(g.A + ip * g.cin + ci);
+        } else {
+            v = ld4(g.A + rc * g.lda + k);
         }
-        return ld4(g.A + row * g.lda + k);
+        return row < g.M ? v : f4{0.f, 0.f, 0.f, 0.f};
     };
     f4 bpre[NP * BV];
     const long wps = long(g.N) * g.K;   // X6: part plane stride
@@ -648,6 +659,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             for (int kg = 0; kg < KG; ++kg) acur[mt][kg] += anext2[mt][kg];
     }
     bstore(0);
+    for (int i = tid; i < g.N; i += 256) bsh[i] = g.bias ? g.bias[i] : 0.0f;
     // The first tile's rows arrive before the loop: with loads still pending on its entry
     // edge, every slice would wait for its own prefetch before its products.
     __builtin_amdgcn_s_waitcnt(0);
@@ -665,13 +677,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         for (int c = 0; c < nch; ++c) {
             const bool last = c + 1 == nch;
             const bool more = !last || tn < tiles;
-            if (!last) {
-                bload(n0, (c + 1) * KC);
-                aload(m0, (c + 1) * KC, anext);
-            } else if (tn < tiles) {
-                bload(n0n, 0);
-                aload(m0n, 0, anext);
-            }
+            // The next slice (the next tile's first at the last slice) is requested on every
+            // path, past the last tile too (then column block 0's weights and rows past the
+            // end, unused): with loads on some paths only, the wait before the products
+            // would have to cover the loads just issued.
+            bload(last ? n0n : n0, last ? 0 : (c + 1) * KC);
+            aload(last ? m0n : m0, last ? 0 : (c + 1) * KC, anext);
+            // ... and kept here, ahead of the products (the scheduler would otherwise sink
+            // them next to their LDS stores at the end of the slice).
+            __builtin_amdgcn_sched_barrier(0);
             if constexpr (RPRE) {
                 if (last) {
 #pragma unroll
@@ -770,7 +784,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
             const int col = n0 + nt * 16 + lg * 4;
-            const f4 bv = g.bias ? ld4(g.bias + col) : f4{0.f, 0.f, 0.f, 0.f};
+            const f4 bv = ld4(bsh + col);
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt) {
                 const long row = m0 + mt * 16 + li;
@@ -890,7 +904,7 @@ static bool launch_gemm3(const GemmArgs& g, GemmA a, GemmE e, hipStream_t s) {
     // k_gemm3 decodes tile indices in 32 bits (at most 2^31 tiles of 16 rows or more). The
     // patch operand with the depth-to-space epilogue (no layer of the network) is left to
     // k_gemm2.
-    if (g.M / 16 >= (1L << 31) || (a == A_S2D && e == E_D2S)) return false;
+    if (g.M / 16 >= (1L << 31) || (a == A_S2D && e == E_D2S) || g.N > GEMM3_NMAX) return false;
     if (g.WX && a != A_LN && g.K % 32 == 0 && g.N % 64 == 0) {
         // Split products: at least two 16-row tiles per wave, so the three weight planes a
         // wave reads from LDS per k block feed twice as many products (one tile per wave
