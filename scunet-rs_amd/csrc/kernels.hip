@@ -4351,30 +4351,34 @@ __global__ __launch_bounds__(T * 2) __attribute__((amdgpu_waves_per_eu(2, 2))) v
             }
         }
     }
+    // The residual rows and the projection bias are all read before the first store (read
+    // per store, each read was waited for between the stores).
+    f4 rres[4][2], bpv[2];
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct) bpv[ct] = ld4(a.bp + c0 + ct * 16 + lg * 4);
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+        const long row = rowof(mt * 16 + li);
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) rres[mt][ct] = ld4(a.x + row * a.ldx + c0 + ct * 16 + lg * 4);
+    }
     if constexpr (!MLP) {
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt) {
             const long row = rowof(mt * 16 + li);
 #pragma unroll
-            for (int ct = 0; ct < 2; ++ct) {
-                float* o = a.x + row * a.ldx + c0 + ct * 16 + lg * 4;
-                st4(o, ld4(o) + (acc[mt][ct] + ld4(a.bp + c0 + ct * 16 + lg * 4)));
-            }
+            for (int ct = 0; ct < 2; ++ct)
+                st4(a.x + row * a.ldx + c0 + ct * 16 + lg * 4, rres[mt][ct] + (acc[mt][ct] + bpv[ct]));
         }
         return;
     } else {
         // The block's rows after the attention residual go to LDS (xs is free: phase 2 is
         // over), so that phase 4 sees whole rows.
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
-            const long row = rowof(mt * 16 + li);
+        for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-            for (int ct = 0; ct < 2; ++ct) {
-                const int col = c0 + ct * 16 + lg * 4;
-                st4(xs + (mt * 16 + li) * LDX + col,
-                    ld4(a.x + row * a.ldx + col) + (acc[mt][ct] + ld4(a.bp + col)));
-            }
-        }
+            for (int ct = 0; ct < 2; ++ct)
+                st4(xs + (mt * 16 + li) * LDX + c0 + ct * 16 + lg * 4, rres[mt][ct] + (acc[mt][ct] + bpv[ct]));
         __syncthreads();
         // 4. The MLP (cpu.rs:800-860) on whole token tiles: wave w takes tiles w, w + HEADS,
         // ... (MT of them); LN2 in registers, the hidden layer 32 units at a time, transposed
@@ -4500,12 +4504,17 @@ __global__ __launch_bounds__(T * 2) __attribute__((amdgpu_waves_per_eu(2, 2))) v
                     }
             }
         }
+        // The output bias is read once, ahead of the stores (read per store, each read was
+        // waited for between them).
+        f4 b2v[KG];
+#pragma unroll
+        for (int nt = 0; nt < KG; ++nt) b2v[nt] = ld4(a.b2 + nt * 16 + lg * 4);
 #pragma unroll
         for (int i = 0; i < MT; ++i) {
             const long row = rowof((wave + i * HEADS) * 16 + li);
 #pragma unroll
             for (int nt = 0; nt < KG; ++nt)
-                st4(a.x + row * a.ldx + nt * 16 + lg * 4, xr[i][nt] + (acc2[i][nt] + ld4(a.b2 + nt * 16 + lg * 4)));
+                st4(a.x + row * a.ldx + nt * 16 + lg * 4, xr[i][nt] + (acc2[i][nt] + b2v[nt]));
         }
     }
 }
