@@ -4658,6 +4658,32 @@ __global__ __launch_bounds__(256) void k_head(const float* __restrict__ x, int c
                 av[kg][s] = ok ? v : 0.0f;
             }
     };
+    if (!add) {
+        // Plain form: the taps of all four pixel groups are requested before the first
+        // product (one round trip per wave instead of one per group).
+        f4 av[4][2];
+#pragma unroll
+        for (int step = 0; step < 4; ++step) gather(step, av[step]);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int step = 0; step < 4; ++step) {
+            const long p = (long(blockIdx.x) * 16 + wave * 4 + step) * 16 + li;
+            f4 acc[4];
+#pragma unroll
+            for (int nt = 0; nt < 4; ++nt) acc[nt] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int kg = 0; kg < 2; ++kg)
+#pragma unroll
+                for (int s = 0; s < 4; ++s)
+#pragma unroll
+                    for (int nt = 0; nt < 4; ++nt) acc[nt] = mfma4(wf[nt][kg][s], av[step][kg][s], acc[nt]);
+            if (p < P) {
+#pragma unroll
+                for (int nt = 0; nt < 4; ++nt) st4(out + p * 64 + lg * 4 + nt * 16, acc[nt]);
+            }
+        }
+        return;
+    }
     f4 cur[2], nxt[2];
     gather(0, cur);
 #pragma unroll
